@@ -1,0 +1,48 @@
+// byhip_gemm.h - host-side launchers of the MFMA GEMM kernels (internal to libbybyhip.so).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace byhip {
+
+// Weight formats of the LDS-staged fp16 MFMA GEMM (y[M, N] = x[M, K] . W^T, fp32 accumulation).
+enum class BFormat {
+    Q4Fast,     // Q4 nibbles, integer zero points, fp16 scales: (q - z) * s rounded once to fp16
+    Q4Generic,  // Q4 nibbles, any zeros / scales / group: ((float)q - z) * s rounded to fp16
+    Fp4Km,      // FP4-KM nibbles + scale bytes + 272-float decode table
+    F16         // IEEE halves [N, K]
+};
+
+struct GemmArgs {
+    const void* x = nullptr;  // [M, K], x_dtype BYHIP_F32 (split into two fp16 terms) or BYHIP_F16
+    int x_dtype = 0;
+    void* y = nullptr;        // [M, N], y_dtype
+    int y_dtype = 0;
+    int M = 0, K = 0, N = 0;
+    // Q4
+    const uint8_t* wq = nullptr;
+    size_t row_bytes = 0;
+    const void* scales = nullptr;
+    int scale_f16 = 0;
+    const float* zeros = nullptr;  // null: zero_value for every group
+    float zero_value = 0.0f;
+    int group = 0;                 // 0: one group per row
+    int gpr = 0;
+    // FP4-KM
+    const uint8_t* blob = nullptr;
+    size_t scale_base = 0;
+    const float* lut = nullptr;    // the 272 floats (16 values, 256 scales)
+    // F16
+    const uint16_t* w16 = nullptr;
+};
+
+// Queues the GEMM on the library stream; K % 32 == 0 is required (callers check).
+void launch_gemm(BFormat fmt, const GemmArgs& a);
+
+// Native MXFP4 GEMM (E2M1 x E2M1 with E8M0 block scales): x and w in the FP4-KM packing.
+// K % 128 == 0 is required.
+void launch_mxfp4(const uint8_t* x, const uint8_t* x_scales, const uint8_t* w,
+                  const uint8_t* w_scales, void* y, int y_dtype, int M, int K, int N);
+
+}  // namespace byhip

@@ -1,0 +1,90 @@
+// byhip_internal.h - shared declarations of libbybyhip.so (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "byhip.h"
+
+namespace byhip {
+
+// A failure that the C ABI reports as BYHIP_ERROR with its message.
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+// A shape or device the entry point does not handle: reported as BYHIP_UNSUPPORTED, the "false"
+// of the reference's encoders.
+struct Unsupported : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+[[noreturn]] void unsupported(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void check_hip(hipError_t e, const char* what, const char* file, int line);
+#define BYHIP_HIP(call) ::byhip::check_hip((call), #call, __FILE__, __LINE__)
+// Checks the launch just queued (invalid configuration and the like).
+#define BYHIP_LAUNCHED(name) ::byhip::check_hip(hipGetLastError(), name, __FILE__, __LINE__)
+
+void set_error(const std::string& msg);
+
+// Every entry point: injected fault first, then the device must be initialised.
+void enter_compute();
+hipStream_t stream();
+int compute_units();
+
+// Allocation registry of buffers the library handed out: byte size (0 = not ours) and, for small
+// host uploads, a host copy (decode tables are classified on the host without a device read).
+size_t alloc_bytes(const void* p);
+const std::vector<uint8_t>* host_mirror(const void* p);
+void* device_alloc(size_t bytes);
+void device_free(void* p);
+// Bounds check of a device pointer the library allocated: [p, p + need) inside its allocation.
+void check_span(const void* p, size_t need, const char* what);
+// Reads `bytes` at `p` to the host, from the mirror when there is one, else with a stream wait.
+void read_small(const void* p, size_t off, void* dst, size_t bytes);
+
+template <class F>
+int guard(F&& f) {
+    try {
+        f();
+        return BYHIP_OK;
+    } catch (const Unsupported& e) {
+        set_error(e.what());
+        return BYHIP_UNSUPPORTED;
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return BYHIP_ERROR;
+    } catch (...) {
+        set_error("byhip: unknown exception");
+        return BYHIP_ERROR;
+    }
+}
+
+inline size_t dtype_bytes(int dt) {
+    switch (dt) {
+    case BYHIP_F32: return 4;
+    case BYHIP_F16: case BYHIP_BF16: return 2;
+    default: return 0;
+    }
+}
+
+}  // namespace byhip
+
+// byhip_q4w: resident Q4 weights in the device layout.
+struct byhip_q4w {
+    int K, N, group, gpr;       // group 0: one group per row (cpu_kernels_impl.inc:309)
+    size_t row_bytes;           // (K + 1) / 2
+    uint8_t* wq;                // nibble rows [N, row_bytes], from byte 0
+    void* scales;               // [N * gpr], fp16 when scale_f16 else fp32
+    float* zeros;               // [N * gpr] fp32, or null when zero_uniform
+    int scale_f16;
+    int zero_uniform;
+    float zero_value;
+    size_t bytes;               // device bytes held
+};

@@ -1,0 +1,414 @@
+// byhip_runtime.hip - device, stream, memory, errors and the session lifecycle of libbybyhip.so.
+//
+// Mirrors the reference's session semantics (gpubackend.nim:894-903, 1042-2721): one open session
+// at a time, uploads into device buffers, work queued on one stream, sessionEnd = wait + error
+// check, frees deferred while a session is open, GPU time from events around each session.
+#include "byhip_internal.h"
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+namespace byhip {
+namespace {
+
+struct Alloc {
+    size_t bytes = 0;
+    std::vector<uint8_t> mirror;  // host copy of a small upload (<= kMirrorBytes)
+};
+
+constexpr size_t kMirrorBytes = 64 * 1024;
+
+struct State {
+    std::recursive_mutex mu;
+    bool inited = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t prop{};
+    std::unordered_map<const void*, Alloc> allocs;
+    // session
+    bool session_open = false;
+    std::vector<void*> deferred_frees;
+    bool timing = false;
+    hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+    double gpu_seconds = 0.0;
+};
+
+State& st() {
+    static State s;
+    return s;
+}
+
+thread_local std::string t_last_error;
+std::atomic<int> g_fault_inject{0};
+
+}  // namespace
+
+void set_error(const std::string& msg) { t_last_error = msg; }
+
+void fail(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw Error(buf);
+}
+
+void unsupported(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw Unsupported(buf);
+}
+
+void check_hip(hipError_t e, const char* what, const char* file, int line) {
+    if (e != hipSuccess) {
+        const char* base = strrchr(file, '/');
+        fail("byhip: %s failed: %s (%s:%d)", what, hipGetErrorString(e), base ? base + 1 : file,
+             line);
+    }
+}
+
+void enter_compute() {
+    int pending = g_fault_inject.load();
+    while (pending > 0) {
+        if (g_fault_inject.compare_exchange_weak(pending, pending - 1))
+            fail("byhip: injected fault");
+    }
+    if (!st().inited) fail("byhip: not initialised (call byhip_init first)");
+}
+
+hipStream_t stream() { return st().stream; }
+int compute_units() { return st().prop.multiProcessorCount; }
+
+size_t alloc_bytes(const void* p) {
+    State& s = st();
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
+    auto it = s.allocs.find(p);
+    return it == s.allocs.end() ? 0 : it->second.bytes;
+}
+
+const std::vector<uint8_t>* host_mirror(const void* p) {
+    State& s = st();
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
+    auto it = s.allocs.find(p);
+    if (it == s.allocs.end() || it->second.mirror.empty()) return nullptr;
+    return &it->second.mirror;
+}
+
+void* device_alloc(size_t bytes) {
+    State& s = st();
+    void* p = nullptr;
+    BYHIP_HIP(hipMalloc(&p, bytes ? bytes : 1));
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
+    s.allocs[p].bytes = bytes;
+    return p;
+}
+
+void device_free(void* p) {
+    if (!p) return;
+    State& s = st();
+    {
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        s.allocs.erase(p);
+    }
+    BYHIP_HIP(hipFree(p));
+}
+
+void check_span(const void* p, size_t need, const char* what) {
+    if (!p) fail("byhip: %s is null", what);
+    State& s = st();
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
+    // Find the allocation holding p (p may point inside one, e.g. a slot at an offset).
+    for (const auto& kv : s.allocs) {
+        const uint8_t* base = static_cast<const uint8_t*>(kv.first);
+        const uint8_t* q = static_cast<const uint8_t*>(p);
+        if (q >= base && q < base + (kv.second.bytes ? kv.second.bytes : 1)) {
+            size_t avail = kv.second.bytes - static_cast<size_t>(q - base);
+            if (need > avail)
+                fail("byhip: %s needs %zu bytes but its buffer holds %zu", what, need, avail);
+            return;
+        }
+    }
+    // Not one of ours (memory from another allocator): the caller vouches for the size.
+}
+
+void read_small(const void* p, size_t off, void* dst, size_t bytes) {
+    if (const std::vector<uint8_t>* m = host_mirror(p)) {
+        if (off + bytes <= m->size()) {
+            memcpy(dst, m->data() + off, bytes);
+            return;
+        }
+    }
+    BYHIP_HIP(hipStreamSynchronize(stream()));
+    BYHIP_HIP(hipMemcpy(dst, static_cast<const uint8_t*>(p) + off, bytes, hipMemcpyDeviceToHost));
+}
+
+}  // namespace byhip
+
+using namespace byhip;
+
+extern "C" {
+
+int byhip_version(void) { return 1; }
+
+const char* byhip_last_error(void) { return t_last_error.c_str(); }
+
+void byhip_clear_error(void) { t_last_error.clear(); }
+
+void byhip_fault_inject(int count) { g_fault_inject.store(count > 0 ? count : 0); }
+
+int byhip_init(int device) {
+    return guard([&] {
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.inited) {
+            if (device != s.device)
+                fail("byhip: already initialised on device %d (asked for %d)", s.device, device);
+            return;
+        }
+        int count = 0;
+        hipError_t e = hipGetDeviceCount(&count);
+        if (e != hipSuccess || count <= 0) fail("byhip: no HIP device is available");
+        if (device < 0 || device >= count) fail("byhip: device %d out of range (%d)", device, count);
+        BYHIP_HIP(hipSetDevice(device));
+        BYHIP_HIP(hipGetDeviceProperties(&s.prop, device));
+        if (strncmp(s.prop.gcnArchName, "gfx950", 6) != 0)
+            fail("byhip: built for gfx950, device %d is %s", device, s.prop.gcnArchName);
+        BYHIP_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+        BYHIP_HIP(hipEventCreate(&s.ev_begin));
+        BYHIP_HIP(hipEventCreate(&s.ev_end));
+        s.device = device;
+        s.inited = true;
+    });
+}
+
+int byhip_device_info_get(byhip_device_info* out) {
+    return guard([&] {
+        enter_compute();
+        if (!out) fail("byhip: null device info");
+        const hipDeviceProp_t& p = st().prop;
+        memset(out, 0, sizeof *out);
+        out->device = st().device;
+        out->compute_units = p.multiProcessorCount;
+        out->wavefront_size = p.warpSize;
+        out->clock_khz = p.clockRate;
+        out->memory_clock_khz = p.memoryClockRate;
+        out->memory_bus_width = p.memoryBusWidth;
+        out->total_global_mem = p.totalGlobalMem;
+        out->lds_bytes_per_block = p.sharedMemPerBlock;
+        snprintf(out->arch_name, sizeof out->arch_name, "%s", p.gcnArchName);
+        snprintf(out->name, sizeof out->name, "%s", p.name);
+    });
+}
+
+int byhip_alloc(size_t bytes, void** dptr) {
+    return guard([&] {
+        enter_compute();
+        if (!dptr) fail("byhip: null output pointer");
+        *dptr = device_alloc(bytes);
+    });
+}
+
+int byhip_free(void* dptr) {
+    return guard([&] {
+        enter_compute();
+        BYHIP_HIP(hipStreamSynchronize(stream()));
+        device_free(dptr);
+    });
+}
+
+int byhip_upload(void* dptr, size_t dst_off, const void* src, size_t bytes) {
+    return guard([&] {
+        enter_compute();
+        if (!bytes) return;
+        if (!src) fail("byhip: null upload source");
+        check_span(static_cast<uint8_t*>(dptr) + dst_off, bytes, "upload destination");
+        BYHIP_HIP(hipMemcpyAsync(static_cast<uint8_t*>(dptr) + dst_off, src, bytes,
+                                 hipMemcpyHostToDevice, stream()));
+        BYHIP_HIP(hipStreamSynchronize(stream()));  // the source is pageable host memory
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        auto it = s.allocs.find(dptr);
+        if (it != s.allocs.end()) {
+            std::vector<uint8_t>& m = it->second.mirror;
+            if (!m.empty()) {
+                if (dst_off + bytes <= m.size())
+                    memcpy(m.data() + dst_off, src, bytes);
+                else
+                    m.clear();
+            }
+        }
+    });
+}
+
+int byhip_read(const void* dptr, size_t src_off, void* dst, size_t bytes) {
+    return guard([&] {
+        enter_compute();
+        if (!bytes) return;
+        if (!dst) fail("byhip: null read destination");
+        check_span(static_cast<const uint8_t*>(dptr) + src_off, bytes, "read source");
+        BYHIP_HIP(hipStreamSynchronize(stream()));
+        BYHIP_HIP(hipMemcpy(dst, static_cast<const uint8_t*>(dptr) + src_off, bytes,
+                            hipMemcpyDeviceToHost));
+    });
+}
+
+int byhip_memset(void* dptr, int value, size_t bytes) {
+    return guard([&] {
+        enter_compute();
+        if (!bytes) return;
+        check_span(dptr, bytes, "memset destination");
+        BYHIP_HIP(hipMemsetAsync(dptr, value, bytes, stream()));
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        auto it = s.allocs.find(dptr);
+        if (it != s.allocs.end()) it->second.mirror.clear();
+    });
+}
+
+int byhip_synchronize(void) {
+    return guard([&] {
+        enter_compute();
+        BYHIP_HIP(hipStreamSynchronize(stream()));
+    });
+}
+
+void* byhip_stream(void) { return st().inited ? static_cast<void*>(st().stream) : nullptr; }
+
+// ── Session ──────────────────────────────────────────────────────────────────────────────────
+
+int byhip_session_begin(void) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) fail("byhip: a session is already open");
+        s.session_open = true;
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+    });
+}
+
+static void* session_new_buffer(const void* data, size_t bytes, bool zero) {
+    void* p = device_alloc(bytes);
+    if (data && bytes) {
+        BYHIP_HIP(hipMemcpyAsync(p, data, bytes, hipMemcpyHostToDevice, stream()));
+        BYHIP_HIP(hipStreamSynchronize(stream()));
+        if (bytes <= kMirrorBytes) {
+            State& s = st();
+            std::lock_guard<std::recursive_mutex> lk(s.mu);
+            std::vector<uint8_t>& m = s.allocs[p].mirror;
+            m.assign(static_cast<const uint8_t*>(data), static_cast<const uint8_t*>(data) + bytes);
+        }
+    } else if (zero && bytes) {
+        BYHIP_HIP(hipMemsetAsync(p, 0, bytes, stream()));
+    }
+    return p;
+}
+
+int byhip_session_upload(const float* data, size_t n, void** out) {
+    return guard([&] {
+        enter_compute();
+        if (!out) fail("byhip: null output handle");
+        if (n && !data) fail("byhip: null upload data");
+        *out = session_new_buffer(data, n * sizeof(float), false);
+    });
+}
+
+int byhip_session_upload_bytes(const void* data, size_t bytes, void** out) {
+    return guard([&] {
+        enter_compute();
+        if (!out) fail("byhip: null output handle");
+        if (bytes && !data) fail("byhip: null upload data");
+        *out = session_new_buffer(data, bytes, false);
+    });
+}
+
+int byhip_session_alloc_scratch(size_t n, void** out) {
+    return guard([&] {
+        enter_compute();
+        if (!out) fail("byhip: null output handle");
+        *out = session_new_buffer(nullptr, n * sizeof(float), true);
+    });
+}
+
+int byhip_session_end(void) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (!s.session_open) fail("byhip: no session is open");
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        hipError_t e = hipStreamSynchronize(s.stream);
+        s.session_open = false;
+        std::vector<void*> frees;
+        frees.swap(s.deferred_frees);
+        if (e != hipSuccess) fail("byhip: session failed on the device: %s", hipGetErrorString(e));
+        if (s.timing) {
+            float ms = 0.0f;
+            BYHIP_HIP(hipEventElapsedTime(&ms, s.ev_begin, s.ev_end));
+            s.gpu_seconds += ms * 1e-3;
+        }
+        for (void* p : frees) device_free(p);
+    });
+}
+
+int byhip_session_commit_continue(void) {
+    return guard([&] {
+        enter_compute();
+        if (!st().session_open) fail("byhip: no session is open");
+        // HIP submits queued work as it is enqueued; nothing to flush and nothing to wait for.
+    });
+}
+
+int byhip_session_recover(void) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        (void)hipStreamSynchronize(s.stream);
+        (void)hipGetLastError();
+        s.session_open = false;
+        std::vector<void*> frees;
+        frees.swap(s.deferred_frees);
+        for (void* p : frees) device_free(p);
+    });
+}
+
+int byhip_session_read(const void* h, float* dst, size_t n) {
+    return byhip_read(h, 0, dst, n * sizeof(float));
+}
+
+int byhip_session_free(void* h) {
+    return guard([&] {
+        enter_compute();
+        if (!h) return;
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) {
+            s.deferred_frees.push_back(h);
+            return;
+        }
+        BYHIP_HIP(hipStreamSynchronize(s.stream));
+        device_free(h);
+    });
+}
+
+int byhip_session_set_gpu_timing(int on) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        s.timing = on != 0;
+        s.gpu_seconds = 0.0;
+    });
+}
+
+double byhip_session_gpu_seconds(void) { return st().gpu_seconds; }
+
+}  // extern "C"

@@ -1,0 +1,222 @@
+"""Q4 block-dequant GEMV / GEMM on the MI355X against the oracle (reference CPU semantics).
+
+Bar: fp32 activations and fp32 accumulation on the decode GEMV match the reference test's own
+tolerance (max|diff| <= 1e-4 * max(1, peak)); the fp16-MFMA GEMM, whose weights are rounded once to
+fp16, meets the fp32-accumulate tier (max-abs-rel <= 1e-3); fp16 outputs are compared after the
+oracle's values are rounded the same way. Unpacked codes and scales are bit-exact.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle_lib import OP_Q4_COOP_GEMM, OP_Q4_GEMV, q4_blob, shape_op_program
+from parity import TIER_F32_ACC, bf16_bits_to_f32, f32_to_bf16_rne, ref_check, tier_check
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+class route:
+    """Forces the library's Q4 route (BYHIP_Q4_ROUTE: 1 GEMV, 2 GEMM, 3 generic) for a block."""
+
+    def __init__(self, r):
+        self.r = r
+
+    def __enter__(self):
+        os.environ["BYHIP_Q4_ROUTE"] = str(self.r)
+
+    def __exit__(self, *a):
+        os.environ.pop("BYHIP_Q4_ROUTE", None)
+
+
+def run_q4(hip, x, wq, sc, ze, M, K, N, grp, x_dtype=None, y_dtype=None, gpr=None):
+    x_dtype = hip.F32 if x_dtype is None else x_dtype
+    y_dtype = hip.F32 if y_dtype is None else y_dtype
+    w = hip.Q4Weights(wq, sc, ze, K, N, grp, gpr if gpr else max(1, K // grp if grp else 1))
+    xd = hip.DeviceBuffer.from_array(np.asarray(x, dtype=hip.np_dtype(x_dtype)).reshape(-1))
+    yd = hip.DeviceBuffer(M * N * (4 if y_dtype == hip.F32 else 2))
+    hip.q4_matmul(xd, x_dtype, w, yd, y_dtype, M)
+    out = yd.read(hip.np_dtype(y_dtype), M * N)
+    if y_dtype == hip.BF16:
+        out = bf16_bits_to_f32(out)
+    return out.astype(np.float32).reshape(M, N), w
+
+
+def golden_q4(i):
+    g = load("q4_cases.npz")
+    M, K, N, grp, sym = (int(v) for v in g[f"shape_{i}"])
+    return M, K, N, grp, g[f"x_{i}"], g[f"wq_{i}"], g[f"scales_{i}"], g[f"zeros_{i}"], g[f"gemv_{i}"]
+
+
+@pytest.mark.parametrize("i", range(10))
+@pytest.mark.parametrize("r", [0, 1, 2, 3])
+def test_q4_golden_routes(hip, i, r):
+    M, K, N, grp, x, wq, sc, ze, want = golden_q4(i)
+    print(f"q4 golden case {i} route {r} M={M} K={K} N={N} group={grp}", flush=True)
+    if r == 2 and K % 32:
+        pytest.skip("GEMM route needs K % 32 == 0")
+    with route(r):
+        got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, grp)
+    if r == 3 or (r in (0, 1) and M <= 8):
+        ref_check(got, want)  # fp32 routes: the reference test's tolerance
+    else:
+        tier_check(got, want, TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_q4_unpack_bit_exact(hip, oracle, i):
+    M, K, N, grp, x, wq, sc, ze, _ = golden_q4(i)
+    w = hip.Q4Weights(wq, sc, ze, K, N, grp, K // grp)
+    codes, s2, z2 = w.unpack()
+    assert np.array_equal(codes, oracle.unpack_q4(wq, K, N))
+    assert np.array_equal(s2.view(np.uint32), sc.view(np.uint32))
+    assert np.array_equal(z2.view(np.uint32), ze.view(np.uint32))
+    info = w.info()
+    sym = bool(load("q4_cases.npz")[f"shape_{i}"][4])
+    assert info["scale_is_f16"] == int(sym) and info["zero_uniform"] == int(sym)
+
+
+@pytest.mark.parametrize("op", [OP_Q4_GEMV, OP_Q4_COOP_GEMM])
+@pytest.mark.parametrize("i", range(10))
+def test_q4_program_route_golden(hip, i, op):
+    """The micro-VM route: the shape op over the one-blob slots (cpu_vm.c:446-450)."""
+    g = load("q4_cases.npz")
+    M, K, N, grp, x, wq, sc, ze, _ = golden_q4(i)
+    key = ("gemv_" if op == OP_Q4_GEMV else "coop_") + str(i)
+    if key not in g:
+        pytest.skip("shape not valid for this op")
+    u8, f32 = q4_blob(wq, sc, ze, K, N, K // grp)
+    mem = hip.DeviceBuffer(M * N * 4)
+    hip.program_dispatch(shape_op_program(op, M, K, N, grp, K // grp), mem,
+                         hip.DeviceBuffer.from_array(u8), hip.DeviceBuffer.from_array(f32),
+                         hip.DeviceBuffer.from_array(x))
+    got = mem.read(np.float32)
+    if M <= 8:
+        ref_check(got, g[key])
+    else:
+        tier_check(got, g[key], TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("x_dtype", ["f32", "f16"])
+@pytest.mark.parametrize("y_dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 64, 130])
+def test_q4_dtypes_and_rows(hip, oracle, M, x_dtype, y_dtype):
+    from bybylang_amd import synth
+    g = synth.rng(1000 + M)
+    K, N = 512, 200
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float32)
+    xt = {"f32": hip.F32, "f16": hip.F16}[x_dtype]
+    yt = {"f32": hip.F32, "f16": hip.F16, "bf16": hip.BF16}[y_dtype]
+    xin = x if x_dtype == "f32" else x.astype(np.float16)
+    print(f"q4 M={M} x={x_dtype} y={y_dtype}", flush=True)
+    got, _ = run_q4(hip, xin, wq, sc, ze, M, K, N, 32, xt, yt)
+    want = oracle.matmul_q4(np.asarray(xin, np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    if y_dtype == "f16":
+        want_r = want.astype(np.float16).astype(np.float32)
+        tier_check(got, want_r, TIER_F32_ACC)
+    elif y_dtype == "bf16":
+        tier_check(got, f32_to_bf16_rne(want).reshape(M, N), 4e-3)
+    elif M <= 8:
+        ref_check(got, want)
+    else:
+        tier_check(got, want, TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("case", ["group0", "group64", "group128", "asym_zero", "int_zero5",
+                                  "f32_scales", "odd_k", "gpr_pad", "k32"])
+@pytest.mark.parametrize("M", [1, 3, 24])
+def test_q4_edge_shapes(hip, oracle, case, M):
+    r = np.random.default_rng(hash(case) % 1000 + M)
+    K, N, grp = 256, 72, 32
+    if case == "group0":
+        grp = 0
+    elif case == "group64":
+        grp = 64
+    elif case == "group128":
+        grp = 128
+    elif case == "odd_k":
+        K = 250
+        grp = 50
+    elif case == "k32":
+        K = 32
+    gpr = 1 if grp == 0 else (K + grp - 1) // grp
+    if case == "gpr_pad":
+        gpr += 3
+    q = r.integers(0, 16, size=(N, K)).astype(np.uint8)
+    if K % 2:
+        q = np.concatenate([q, np.zeros((N, 1), np.uint8)], axis=1)
+    wq = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8).reshape(-1)
+    sc = (np.abs(r.normal(0, 0.02, N * gpr)) + 1e-4).astype(np.float16).astype(np.float32)
+    ze = np.full(N * gpr, 8.0, np.float32)
+    if case == "asym_zero":
+        ze = (r.random(N * gpr) * 15).astype(np.float32)
+    if case == "int_zero5":
+        ze[:] = 5.0
+    if case == "f32_scales":
+        sc = (r.random(N * gpr) * 0.05 + 1e-3).astype(np.float32)
+    x = r.standard_normal(M * K).astype(np.float32)
+    print(f"q4 edge {case} M={M} K={K} group={grp} gpr={gpr}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, grp, gpr=gpr)
+    want = oracle.matmul_q4(x, wq, sc, ze, M, K, N, grp, gpr)
+    if M <= 8:
+        ref_check(got, want)
+    else:
+        tier_check(got, want, TIER_F32_ACC)
+
+
+def test_q4_decode_config_full(hip, oracle):
+    """Config 1 at full size: M=1, K=4096, N=14336, fp16 x, fp16 y, against the oracle."""
+    from bybylang_amd import synth
+    g = synth.rng(0)
+    M, K, N = 1, 4096, 14336
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, hip.F16)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    r = tier_check(got, want.astype(np.float16).astype(np.float32), 1e-3)
+    print(f"c1 max-abs-rel vs fp16-rounded oracle {r:.2e}")
+
+
+def test_q4_prefill_config_rows(hip, oracle):
+    """Config 2 (M=512, K=N=4096, fp16 in/out) on the GPU; rows 0-7 and the last 8 against the
+    oracle, and every row against an fp64 product of the fp16-rounded weights."""
+    from bybylang_amd import synth
+    g = synth.rng(2)
+    M, K, N = 512, 4096, 4096
+    wq, sc, ze, codes = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, hip.F16)
+    xf = x.astype(np.float32).reshape(-1)
+    for r0 in (0, M - 8):
+        want = oracle.matmul_q4(xf, wq, sc, ze, M, K, N, 32, K // 32, rows=(r0, r0 + 8))[r0:r0 + 8]
+        tier_check(got[r0:r0 + 8], want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+    w = (codes.astype(np.float32) * np.repeat(sc.reshape(N, -1), 32, axis=1)).astype(np.float64)
+    full = x.astype(np.float64) @ w.T
+    tier_check(got, full, TIER_F32_ACC)
+
+
+def test_q4_gemv_rotating_copies_consistent(hip):
+    """Independent weight copies (the benchmark's rotation) give identical outputs."""
+    from bybylang_amd import synth
+    g = synth.rng(5)
+    K, N = 4096, 1024
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, 1, K, np.float16)
+    a, _ = run_q4(hip, x, wq, sc, ze, 1, K, N, 32, hip.F16, hip.F32)
+    b, _ = run_q4(hip, x, wq, sc, ze, 1, K, N, 32, hip.F16, hip.F32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_gpu_matmul_q4_immediate(hip, oracle):
+    """gpuMatmulQ4 (host in/out, weights uploaded per call) through the session mirror."""
+    from bybylang_amd import gpubackend as gb
+    M, K, N, grp, x, wq, sc, ze, want = golden_q4(5)
+    got = gb.gpuMatmulQ4(gb.gbHip, x, wq, sc, ze, M, K, N, grp, K // grp)
+    ref_check(got, oracle.matmul_q4(x, wq, sc, ze, M, K, N, grp, K // grp))
