@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of BybyLang's quantized tile-GEMM path on one MI355X (libbybyhip.so).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,c3,c4]
+
+Prints ONE JSON line. The headline (`value`) is config 1 of BASELINE.json: the decode Q4 GEMV
+(M=1, K=4096, N=14336, block-32 Q4 weights with fp16 scales, fp16 x and y, fp32 accumulation) in
+GB/s of algorithmic bytes, inputs resident in HBM. A step is one GEMV launch; K launches are
+recorded as one HIP graph (the session record / replay route) cycling through 16 resident copies of
+the weights (529 MB, more than twice the 256 MB Infinity Cache, so the reads come from HBM), and
+timed with HIP events on the library stream. The other configurations (prefill Q4 GEMM, MXFP4
+GEMM, the decoder-layer batch) are reported under "configs" with the same method.
+
+cpu_baseline: the reference's own CPU path for this op (nimf_cpu_matmul_q4,
+backends/cpu/cpu_kernels_impl.inc:293-319, compiled from its sources into oracle/_ref), single
+threaded as the reference runs, timed on full config-1 passes for about ten seconds; when that
+library is absent, the C restatement in oracle/ ("port").
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+FP16_PEAK_TFLOPS = 2500.0    # dense fp16 / bf16 MFMA
+FP4_PEAK_TFLOPS = 10100.0    # dense fp4 MFMA
+ROTATE_BYTES = 512 << 20     # weight copies past the 256 MB Infinity Cache
+
+
+def q4_bytes(M, K, N):
+    """Algorithmic bytes of a Q4 GEMV/GEMM in the benchmark format: nibbles, one fp16 scale per
+    32 weights, fp16 x and y."""
+    return N * K // 2 + N * (K // 32) * 2 + M * K * 2 + M * N * 2
+
+
+def mx_bytes(M, K, N):
+    return M * K // 2 + M * K // 32 + N * K // 2 + N * K // 32 + M * N * 2
+
+
+class Recorder:
+    """Records `fn(step)` for `count` steps as one session recording (a HIP graph)."""
+
+    def __init__(self, fn, count):
+        from bybylang_amd import gpubackend as gb
+        self.gb = gb
+        assert gb.sessionBeginRecording(gb.gbHip), gb.sessionGetLastError(gb.gbHip)
+        for i in range(count):
+            fn(i)
+        assert gb.sessionEnd(gb.gbHip), gb.sessionGetLastError(gb.gbHip)
+        self.id = gb.sessionLastRecording(gb.gbHip)
+        assert self.id >= 0
+
+    def timed(self, times=1) -> float:
+        """Replays and returns the GPU seconds between the events around the launches."""
+        gb = self.gb
+        assert gb.sessionSetGpuTiming(gb.gbHip, True)
+        assert gb.sessionReplay(gb.gbHip, self.id, times), gb.sessionGetLastError(gb.gbHip)
+        t = gb.sessionGpuSeconds(gb.gbHip)
+        gb.sessionSetGpuTiming(gb.gbHip, False)
+        return t
+
+    def close(self):
+        self.gb.sessionFreeRecording(self.gb.gbHip, self.id)
+
+
+def run_steps(fn, steps, warmup):
+    """Warmup recording replayed once, then the timed recording of exactly `steps` steps."""
+    if warmup > 0:
+        w = Recorder(fn, warmup)
+        w.timed()
+        w.close()
+    r = Recorder(fn, steps)
+    wall0 = time.perf_counter()
+    gpu_s = r.timed()
+    wall = time.perf_counter() - wall0
+    r.close()
+    return gpu_s, wall
+
+
+def q4_setup(dev, synth, seed, M, K, N, copies):
+    g = synth.rng(seed)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    ws = [dev.Q4Weights(wq, sc, ze, K, N, 32, K // 32) for _ in range(copies)]
+    x = dev.DeviceBuffer.from_array(synth.activations(g, M, K, np.float16).reshape(-1))
+    y = dev.DeviceBuffer(M * N * 2)
+    return ws, x, y
+
+
+def bench_c1(dev, synth, steps, warmup):
+    M, K, N = 1, 4096, 14336
+    nbytes = q4_bytes(M, K, N)
+    copies = max(1, -(-ROTATE_BYTES // nbytes))
+    ws, x, y = q4_setup(dev, synth, 1, M, K, N, copies)
+    fn = lambda i: dev.q4_matmul(x, dev.F16, ws[i % copies], y, dev.F16, M)  # noqa: E731
+    gpu_s, wall = run_steps(fn, steps, warmup)
+    per = gpu_s / steps
+    res = {"M": M, "K": K, "N": N, "bytes_per_step": nbytes, "weight_copies": copies,
+           "rotation_bytes": nbytes * copies, "us_per_step": per * 1e6,
+           "GBps": nbytes / per / 1e9, "TFLOPs": 2 * M * K * N / per / 1e12,
+           "wall_us_per_step": wall / steps * 1e6}
+    for w in ws:
+        w.close()
+    return res
+
+
+def bench_c2(dev, synth, steps, warmup):
+    M, K, N = 512, 4096, 4096
+    ws, x, y = q4_setup(dev, synth, 2, M, K, N, 1)
+    fn = lambda i: dev.q4_matmul(x, dev.F16, ws[0], y, dev.F16, M)  # noqa: E731
+    gpu_s, wall = run_steps(fn, steps, warmup)
+    per = gpu_s / steps
+    flops = 2 * M * K * N
+    return {"M": M, "K": K, "N": N, "flops_per_step": flops, "bytes_per_step": q4_bytes(M, K, N),
+            "us_per_step": per * 1e6, "TFLOPs": flops / per / 1e12,
+            "frac_fp16_peak": flops / per / 1e12 / FP16_PEAK_TFLOPS, "GBps": q4_bytes(M, K, N) / per / 1e9}
+
+
+def bench_c3(dev, synth, steps, warmup):
+    M, K, N = 2048, 8192, 8192
+    g = synth.rng(3)
+    xb, _, _ = synth.mxfp4_operand(g, M, K)
+    wb, _, _ = synth.mxfp4_operand(g, N, K)
+    x = dev.DeviceBuffer.from_array(xb)
+    w = dev.DeviceBuffer.from_array(wb)
+    y = dev.DeviceBuffer(M * N * 2)
+    fn = lambda i: dev.mxfp4_gemm(x, w, y, dev.BF16, M, K, N)  # noqa: E731
+    gpu_s, wall = run_steps(fn, steps, warmup)
+    per = gpu_s / steps
+    flops = 2 * M * K * N
+    return {"M": M, "K": K, "N": N, "flops_per_step": flops, "bytes_per_step": mx_bytes(M, K, N),
+            "us_per_step": per * 1e6, "TFLOPs": flops / per / 1e12,
+            "frac_fp4_peak": flops / per / 1e12 / FP4_PEAK_TFLOPS}
+
+
+C4_OPS = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 2 * 14336), ("down", 14336, 4096)]
+
+
+def bench_c4(dev, synth, steps, warmup):
+    out = {}
+    layer_bytes = {M: sum(q4_bytes(M, K, N) for _, K, N in C4_OPS) for M in (1, 32, 256)}
+    copies = max(1, -(-ROTATE_BYTES // layer_bytes[1]))
+    g = synth.rng(4)
+    weights = []
+    for name, K, N in C4_OPS:
+        wq, sc, ze, _ = synth.q4_weights(g, N, K)
+        weights.append([dev.Q4Weights(wq, sc, ze, K, N, 32, K // 32) for _ in range(copies)])
+    for M in (1, 32, 256):
+        xs = [dev.DeviceBuffer.from_array(synth.activations(g, M, K, np.float16).reshape(-1))
+              for _, K, _ in C4_OPS]
+        ys = [dev.DeviceBuffer(M * N * 2) for _, _, N in C4_OPS]
+        per_op = {}
+        for j, (name, K, N) in enumerate(C4_OPS):
+            fn = lambda i, j=j: dev.q4_matmul(xs[j], dev.F16, weights[j][i % copies], ys[j], dev.F16, M)  # noqa: E731
+            gpu_s, _ = run_steps(fn, steps, warmup)
+            per = gpu_s / steps
+            b, f = q4_bytes(M, K, N), 2 * M * K * N
+            per_op[name] = {"us": per * 1e6, "GBps": b / per / 1e9, "TFLOPs": f / per / 1e12}
+
+        def layer(i):
+            for j in range(len(C4_OPS)):
+                dev.q4_matmul(xs[j], dev.F16, weights[j][i % copies], ys[j], dev.F16, M)
+
+        gpu_s, _ = run_steps(layer, steps, warmup)
+        per = gpu_s / steps
+        flops = sum(2 * M * K * N for _, K, N in C4_OPS)
+        out[f"M{M}"] = {"per_op": per_op, "batch_us": per * 1e6,
+                        "batch_GBps": layer_bytes[M] / per / 1e9, "batch_TFLOPs": flops / per / 1e12}
+    for ws in weights:
+        for w in ws:
+            w.close()
+    out["weight_copies"] = copies
+    return out
+
+
+def cpu_baseline(seconds: float = 10.0):
+    """The reference's single-threaded CPU Q4 matmul (or the oracle port) on full config-1 passes."""
+    from bybylang_amd import synth
+    ref = os.path.join(ROOT, "oracle", "_ref", "libbybyref.so")
+    port = os.path.join(ROOT, "oracle", "liboracle.so")
+    if os.path.exists(ref):
+        lib = C.CDLL(ref)
+        fn, kind = lib.refshim_matmul_q4, "reference"
+        fn.argtypes = [C.c_void_p] * 5 + [C.c_int] * 5
+        call = lambda a, w, s, z, c: fn(a, w, s, z, c, M, K, N, 32, K // 32)  # noqa: E731
+    elif os.path.exists(port):
+        lib = C.CDLL(port)
+        fn, kind = lib.orc_matmul_q4, "port"
+        fn.argtypes = [C.c_void_p] * 5 + [C.c_int] * 7
+        call = lambda a, w, s, z, c: fn(a, w, s, z, c, M, K, N, 32, K // 32, 0, M)  # noqa: E731
+    else:
+        return None
+    M, K, N = 1, 4096, 14336
+    g = synth.rng(1)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    a = synth.activations(g, M, K, np.float16).astype(np.float32).reshape(-1)
+    c = np.zeros(M * N, np.float32)
+    ptrs = [v.ctypes.data for v in (a, wq, sc, ze, c)]
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        call(*ptrs)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / passes
+    return {"value": q4_bytes(M, K, N) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{passes} full config-1 passes (M=1 K=4096 N=14336, fp32 x) in {el:.1f} s, "
+                      f"{per * 1e3:.1f} ms each, nimf_cpu_matmul_q4 single thread on "
+                      f"{platform.processor() or platform.machine()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--configs", default="c1,c2,c3,c4",
+                    help="configurations to measure (c1 is the headline and always runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        sys.stderr.write("bench.py measures one GPU only: this build has no multi-GPU path "
+                         "(collectives are out of scope); run with --gpus 1\n")
+        return 2
+    if args.steps < 1:
+        sys.stderr.write("--steps must be >= 1\n")
+        return 2
+
+    from bybylang_amd import device as dev
+    from bybylang_amd import synth
+    dev.init(0)
+    info = dev.device_info()
+    wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
+
+    c1 = bench_c1(dev, synth, args.steps, args.warmup)
+    configs = {}
+    if "c2" in wanted:
+        configs["c2_prefill_q4_gemm"] = bench_c2(dev, synth, args.steps, args.warmup)
+    if "c3" in wanted:
+        configs["c3_mxfp4_gemm"] = bench_c3(dev, synth, args.steps, args.warmup)
+    if "c4" in wanted:
+        configs["c4_layer_batch"] = bench_c4(dev, synth, max(1, args.steps // 5), max(0, args.warmup // 5))
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+
+    per_s = c1["us_per_step"] * 1e-6
+    line = {
+        "metric": "Q4 GEMV GB/s (% HBM peak) at M=1; Q4/FP4 GEMM TFLOP/s (% MFMA peak) M>=512",
+        "value": round(c1["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c1["us_per_step"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded PCG64: int4 codes uniform [-8,7], fp16 scales |N(0,0.02)|+1e-4, x ~ N(0,1))",
+        "config": {"workload": "c1 decode Q4 GEMV: M=1 K=4096 N=14336, block-32 Q4 + fp16 scales, "
+                               "fp16 x/y, fp32 accumulate",
+                   "weight_copies": c1["weight_copies"], "rotation_bytes": c1["rotation_bytes"],
+                   "timing": "one HIP-graph replay of `steps` launches, hipEvents on the library stream",
+                   "device": info.get("name", ""), "arch": info.get("arch_name", ""),
+                   "compute_units": info.get("compute_units")},
+        "roofline": {"bound": "hbm", "achieved": round(c1["GBps"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(c1["GBps"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "q4_gemv_dot2",
+                     "bytes_per_launch": c1["bytes_per_step"], "avg_launch_us": round(c1["us_per_step"], 3)},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -68,6 +68,11 @@ SIGNATURES = {
     "byhip_session_free": (_I, [_VP]),
     "byhip_session_set_gpu_timing": (_I, [_I]),
     "byhip_session_gpu_seconds": (C.c_double, []),
+    "byhip_session_can_record": (_I, []),
+    "byhip_session_begin_recording": (_I, []),
+    "byhip_session_last_recording": (_I, []),
+    "byhip_session_replay": (_I, [_I, _I]),
+    "byhip_session_free_recording": (_I, [_I]),
     "byhip_q4_resident_upload": (_I, [_U8P, _SZ, _SZ, _FP, _FP, _I, _I, _I, _I, C.POINTER(_VP)]),
     "byhip_q4_resident_from_device": (_I, [_VP, _SZ, _VP, _VP, _I, _I, _I, _I, C.POINTER(_VP)]),
     "byhip_q4_resident_free": (_I, [_VP]),
@@ -82,6 +87,7 @@ SIGNATURES = {
                                     _VP, _SZ, _I]),
     "byhip_debug_unpack_q4": (_I, [_VP, _U8P, _FP, _FP]),
     "byhip_debug_unpack_fp4km": (_I, [_U8P, _SZ, _FP, _SZ, _I, _I, _U8P, _FP]),
+    "byhip_debug_copy": (_I, [_VP, _VP, _SZ]),
 }
 
 _lib = None

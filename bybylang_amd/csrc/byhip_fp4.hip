@@ -231,6 +231,7 @@ int byhip_tile_gemm_ready(int f16, int tensor_core) {
     int result = BYHIP_ERROR;
     const int rc = guard([&] {
         enter_compute();
+        no_host_sync("byhip_tile_gemm_ready");
         (void)tensor_core;  // every HIP route is an MFMA route
         int& c = cache[f16 ? 1 : 0];
         if (c < 0) c = run_ready_gate(f16 != 0) ? 1 : 0;
@@ -315,6 +316,7 @@ int byhip_debug_unpack_fp4km(const uint8_t* blob, size_t scale_base, const float
                              int K, int N, uint8_t* codes, float* weights) {
     return guard([&] {
         enter_compute();
+        no_host_sync("byhip_debug_unpack_fp4km");
         if (!blob || !lut || !codes || !weights || K <= 0 || N <= 0 || K % 32)
             fail("byhip: invalid FP4-KM unpack arguments");
         check_span(blob, scale_base + (size_t)N * (K / 32), "FP4-KM blob");

@@ -1,0 +1,423 @@
+// byhip_gemv.hip - the Q4 decode GEMV (M <= 8) for resident or slot-bound Q4 weights (gfx950).
+//
+// y[m, n] = sum_k x[m, k] * ((float)q[n, k] - zero[n, g]) * scale[n, g] with fp32 accumulation
+// (cpu_kernels_impl.inc:293-319, cpu_vm.c:420-482).
+//
+// Work split: a wave owns R consecutive weight rows (8 when a row is at most two 32-value chunks per
+// lane); lane l holds chunks l, l + 64, ... of every row, each chunk one 16-byte load of 32 nibbles.
+// Per wave the loads go out in this order, all before the first wait: the block's activations, the
+// scales (one 16-byte load per chunk covers 8 rows in the resident layout), then the weight rows;
+// the wait counter completes in issue order, so row r is processed as soon as it lands.
+//
+// Activations are staged once per 256-thread block in LDS: each 32-value chunk as 16 fp16 pairs
+// (x[8j+i], x[8j+i+4]) matching the nibble pairs below, with its sums of x.
+//
+// Nibble pairs become fp16 with one AND-OR against an exponent word: 0x6400 | q is 1024 + q and
+// 0x5400 | (q << 4) is 64 + q, both exact; v_dot2_f32_f16 multiplies them with the x pairs (exact
+// products, fp32 accumulation). With fp16 activations the biased halves go into the dot products
+// and the bias (1024 and 64 times the chunk's sums of x over the low and high nibble pairs) is
+// removed once per chunk; the fp32 sum then carries about 2^-13 of the bias as rounding, well below
+// the fp16 output's own. With fp32 activations the bias is subtracted from the halves first (exact)
+// and x is split into two fp16 terms (hi + lo, ~22 bits). The zero point enters once per chunk as
+// s * (sum x*q - z * sum x).
+#include <algorithm>
+
+#include "byhip_gemv.h"
+#include "byhip_internal.h"
+#include "byhip_kernels.h"
+
+namespace byhip {
+namespace {
+
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Weight rows a wave keeps in flight: 8 rows of up to two chunks per lane, fewer when each row
+// needs more chunks (16 chunk loads in flight per lane at most).
+constexpr int gemv_rows(int cpl) { return cpl >= 8 ? 2 : (cpl >= 4 ? 4 : 8); }
+
+struct GemvArgs {
+    const void* x;
+    const uint8_t* wq;
+    const void* scales;  // resident: [ceil(N/8)][K/32][8]; slots: [N][gpr]
+    const float* zeros;  // same layout as scales (fp32); null when the zero point is uniform
+    float zero_value;
+    void* y;
+    int K, N, group_chunks, gpr, row_bytes, n_pad;
+};
+
+template <int NB>
+__device__ __forceinline__ void load_bytes(rsrc_t r, uint32_t off, uint32_t* w) {
+    if constexpr (NB == 4) {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else if constexpr (NB == 8) {
+        const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        w[0] = v[0]; w[1] = v[1];
+    } else if constexpr (NB == 16) {
+        const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    } else {
+        static_assert(NB == 32, "scale block width");
+        const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        const v4u u = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+        w[4] = u[0]; w[5] = u[1]; w[6] = u[2]; w[7] = u[3];
+    }
+}
+
+template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK, int YT>
+__global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
+    constexpr int XS = XF32 ? 2 : 1;
+    constexpr int R = gemv_rows(CPL);
+    constexpr uint32_t XB = XF32 ? 4 : 2;  // bytes per activation
+    constexpr int XW = XF32 ? 8 : 4;       // 16-byte activation loads per 32-value chunk
+    constexpr int XC = 2;                  // activation chunks a thread stages (M * G <= 512)
+    constexpr uint32_t SB = SF16 ? 2u : 4u;
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int K = a.K, N = a.N, G = K >> 5;
+    const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * R);
+    const bool rows_live = n0 < N;  // uniform in the wave; every wave takes part in the barrier
+
+    uint32_t* xh = lds;                                   // [M][G][16] fp16 pairs
+    uint32_t* xl = xh + M * G * 16;                       // [M][G][16] low terms (fp32 x only)
+    float* sums = reinterpret_cast<float*>(xl + (XS == 2 ? M * G * 16 : 0));  // [M][G]{bias, sum}
+
+    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)N * (uint32_t)a.row_bytes);
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * XB);
+    const uint32_t srows = BLK ? (uint32_t)a.n_pad : (uint32_t)N;
+    const rsrc_t sr = make_rsrc(a.scales, srows * (uint32_t)(BLK ? G : a.gpr) * SB);
+    const rsrc_t zr = make_rsrc(ZU ? a.scales : a.zeros, ZU ? 0u : srows * (uint32_t)(BLK ? G : a.gpr) * 4u);
+
+    // This lane's chunks (chunks past K are clamped onto the last one and their scale is zeroed).
+    uint32_t coff[CPL], gsel[CPL];
+    bool cv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int ci = lane + kWave * c;
+        cv[c] = ci < G;
+        const int cc = min(ci, G - 1);
+        coff[c] = (uint32_t)cc * 16u;
+        gsel[c] = BLK ? (uint32_t)cc : (uint32_t)(a.group_chunks ? cc / a.group_chunks : 0);
+    }
+
+    // 1. the activations this thread stages (chunks tid and tid + 256 of the M x G chunks)
+    uint4 xraw[XC][XW];
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int idx = tid + 256 * i;
+        const int m = idx / G, ci = idx - m * G;
+        const uint32_t base = idx < M * G ? (uint32_t)m * K * XB + (uint32_t)ci * 32u * XB : kOutOfRange;
+#pragma unroll
+        for (int t = 0; t < XW; ++t) xraw[i][t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
+    }
+
+    // 2. scales and zeros of the wave's R rows
+    uint32_t sraw[R][CPL], zraw[R][CPL];
+    // first row of the batch; a wave past the end reads the last (aligned) batch and stores nothing
+    const int nb = BLK ? min(n0, a.n_pad - R) : min(n0, N - 1);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        if constexpr (BLK) {
+            // rows n0 .. n0+R-1 of chunk c sit together: [(n0/8) * G + chunk] * 8 + n0 % 8
+            const uint32_t e = ((uint32_t)(nb >> 3) * (uint32_t)G + gsel[c]) * 8u + (uint32_t)(nb & 7);
+            uint32_t sw[R * SB / 4];
+            load_bytes<R * SB>(sr, e * SB, sw);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                sraw[r][c] = SF16 ? ((sw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu) : sw[r];
+            if constexpr (!ZU) {
+                uint32_t zw[R];
+                load_bytes<R * 4>(zr, e * 4u, zw);
+#pragma unroll
+                for (int r = 0; r < R; ++r) zraw[r][c] = zw[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t g = (uint32_t)min(nb + r, N - 1) * (uint32_t)a.gpr + gsel[c];
+                if constexpr (SF16)
+                    sraw[r][c] = __builtin_amdgcn_raw_buffer_load_b16(sr, g * SB, 0, 0);
+                else
+                    sraw[r][c] = __builtin_amdgcn_raw_buffer_load_b32(sr, g * SB, 0, 0);
+                if constexpr (!ZU) zraw[r][c] = __builtin_amdgcn_raw_buffer_load_b32(zr, g * 4u, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. the weight rows in row order (streamed once: non-temporal); the row offset is
+    // wave-uniform and travels in the scalar offset
+    uint4 wv[R][CPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t roff = (uint32_t)min(nb + r, N - 1) * (uint32_t)a.row_bytes;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wr, coff[c], roff, 2);
+            wv[r][c] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load is out before the first wait
+
+    // 4. stage the activations: fp16 pairs matching the nibble pairs, and the chunk sums
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int idx = tid + 256 * i;
+        if (idx < M * G) {
+            uint32_t p[16], lo[16];
+            float bias = 0.0f, s = 0.0f;
+            if constexpr (XF32) {
+                float v[32];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    v[4 * t] = __builtin_bit_cast(float, xraw[i][t].x);
+                    v[4 * t + 1] = __builtin_bit_cast(float, xraw[i][t].y);
+                    v[4 * t + 2] = __builtin_bit_cast(float, xraw[i][t].z);
+                    v[4 * t + 3] = __builtin_bit_cast(float, xraw[i][t].w);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float u = v[8 * j + q], w = v[8 * j + q + 4];
+                        const _Float16 hu = (_Float16)u, hw = (_Float16)w;
+                        const _Float16 lu = (_Float16)(u - (float)hu), lw = (_Float16)(w - (float)hw);
+                        p[4 * j + q] = (uint32_t)h_bits(hu) | ((uint32_t)h_bits(hw) << 16);
+                        lo[4 * j + q] = (uint32_t)h_bits(lu) | ((uint32_t)h_bits(lw) << 16);
+                    }
+#pragma unroll
+                for (int t = 0; t < 32; ++t) s += v[t];
+            } else {
+                uint32_t d[16];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    d[4 * t] = xraw[i][t].x; d[4 * t + 1] = xraw[i][t].y;
+                    d[4 * t + 2] = xraw[i][t].z; d[4 * t + 3] = xraw[i][t].w;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t A = d[4 * j], B = d[4 * j + 1], C = d[4 * j + 2], D = d[4 * j + 3];
+                    p[4 * j + 0] = __builtin_amdgcn_perm(C, A, 0x05040100u);
+                    p[4 * j + 1] = __builtin_amdgcn_perm(C, A, 0x07060302u);
+                    p[4 * j + 2] = __builtin_amdgcn_perm(D, B, 0x05040100u);
+                    p[4 * j + 3] = __builtin_amdgcn_perm(D, B, 0x07060302u);
+                }
+                // sums over the low-nibble pairs (p[4j], p[4j+2]) and high-nibble pairs (p[4j+1],
+                // p[4j+3]): exact products with 1, fp32 accumulation
+                const h2 one = {1, 1};
+                float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sl = __builtin_amdgcn_fdot2(bits_h2(p[4 * j + 0]), one, sl, false);
+                    sl = __builtin_amdgcn_fdot2(bits_h2(p[4 * j + 2]), one, sl, false);
+                    sh = __builtin_amdgcn_fdot2(bits_h2(p[4 * j + 1]), one, sh, false);
+                    sh = __builtin_amdgcn_fdot2(bits_h2(p[4 * j + 3]), one, sh, false);
+                }
+                s = sl + sh;
+                bias = 1024.0f * sl + 64.0f * sh;
+            }
+            uint4* dh = reinterpret_cast<uint4*>(xh + idx * 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) dh[t] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
+            if constexpr (XS == 2) {
+                uint4* dl = reinterpret_cast<uint4*>(xl + idx * 16);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) dl[t] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
+            }
+            sums[2 * idx] = bias;
+            sums[2 * idx + 1] = s;
+        }
+    }
+    __syncthreads();
+    if (!rows_live) return;
+
+    uint32_t xp[M][CPL][16];
+    uint32_t xq[XS == 2 ? M : 1][XS == 2 ? CPL : 1][16];
+    float bias[M][CPL], sx[M][CPL];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = m * G + (int)(coff[c] >> 4);
+            const uint4* sh = reinterpret_cast<const uint4*>(xh + idx * 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint4 u = sh[t];
+                xp[m][c][4 * t] = u.x; xp[m][c][4 * t + 1] = u.y; xp[m][c][4 * t + 2] = u.z; xp[m][c][4 * t + 3] = u.w;
+            }
+            if constexpr (XS == 2) {
+                const uint4* sl = reinterpret_cast<const uint4*>(xl + idx * 16);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint4 u = sl[t];
+                    xq[m][c][4 * t] = u.x; xq[m][c][4 * t + 1] = u.y; xq[m][c][4 * t + 2] = u.z; xq[m][c][4 * t + 3] = u.w;
+                }
+            }
+            bias[m][c] = sums[2 * idx];
+            sx[m][c] = sums[2 * idx + 1];
+        }
+
+    // Nibble n at bits 0-3 of a half: 0x6400 | n is the fp16 1024 + n; at bits 4-7: 0x5400 | (n << 4)
+    // is the fp16 64 + n. The magic words live in VGPRs so the AND-OR is one v_and_or_b32.
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
+    const h2 bias_lo = {1024, 1024}, bias_hi = {64, 64};
+
+    // 5. rows in load order; each row is reduced over the wave and stored before the next
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t dw[4] = {wv[r][c].x, wv[r][c].y, wv[r][c].z, wv[r][c].w};
+            h2 q[16];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t d8 = dw[w] >> 8;
+                q[4 * w + 0] = bits_h2((dw[w] & 0x000F000Fu) | mag_lo);
+                q[4 * w + 1] = bits_h2((dw[w] & 0x00F000F0u) | mag_hi);
+                q[4 * w + 2] = bits_h2((d8 & 0x000F000Fu) | mag_lo);
+                q[4 * w + 3] = bits_h2((d8 & 0x00F000F0u) | mag_hi);
+                if constexpr (XS == 2) {  // fp32 activations: remove the bias exactly here
+                    q[4 * w + 0] -= bias_lo;
+                    q[4 * w + 1] -= bias_hi;
+                    q[4 * w + 2] -= bias_lo;
+                    q[4 * w + 3] -= bias_hi;
+                }
+            }
+            float s = SF16 ? (float)bits_h((uint16_t)sraw[r][c]) : __builtin_bit_cast(float, sraw[r][c]);
+            s = cv[c] ? s : 0.0f;
+            const float z = ZU ? a.zero_value : __builtin_bit_cast(float, zraw[r][c]);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float p = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    p = __builtin_amdgcn_fdot2(bits_h2(xp[m][c][e]), q[e], p, false);
+                    if constexpr (XS == 2) p = __builtin_amdgcn_fdot2(bits_h2(xq[m][c][e]), q[e], p, false);
+                }
+                acc[m] = fmaf(s, (p - bias[m][c]) - z * sx[m][c], acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float t = wave_sum_lane63(acc[m]);
+            if (lane == 63 && n0 + r < N) store_y<YT>(a.y, (size_t)m * N + n0 + r, t);
+        }
+    }
+}
+
+template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK>
+void launch_y(const GemvArgs& a, int y_dtype) {
+    constexpr int R = gemv_rows(CPL);
+    const int G = a.K / 32;
+    const size_t lds = (size_t)M * G * 16 * 4 * (XF32 ? 2 : 1) + (size_t)M * G * 2 * 4;
+    const int grid = (a.N + 4 * R - 1) / (4 * R);  // one batch of rows per wave
+    switch (y_dtype) {
+    case BYHIP_F32:
+        hipLaunchKernelGGL((q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_F32>), dim3(grid), dim3(256), lds, stream(), a);
+        break;
+    case BYHIP_F16:
+        hipLaunchKernelGGL((q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_F16>), dim3(grid), dim3(256), lds, stream(), a);
+        break;
+    default:
+        hipLaunchKernelGGL((q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_BF16>), dim3(grid), dim3(256), lds, stream(), a);
+        break;
+    }
+    BYHIP_LAUNCHED("q4_gemv");
+}
+
+template <int M, int CPL, bool XF32>
+void launch_szb(const GemvArgs& a, const byhip_q4w* w, bool blk, int y_dtype) {
+    if constexpr (M * CPL * (XF32 ? 2 : 1) > 8) {
+        fail("byhip: internal: GEMV register tile out of range");
+    } else {
+        const bool sf = blk ? w->blk_scale_f16 : w->scale_f16;
+        const bool zu = w->zero_uniform;
+#define BYHIP_GEMV_CASE(SF, ZU_, BLK_) \
+    if (sf == SF && zu == ZU_ && blk == BLK_) return launch_y<M, CPL, XF32, SF, ZU_, BLK_>(a, y_dtype);
+        BYHIP_GEMV_CASE(true, true, true)
+        BYHIP_GEMV_CASE(true, false, true)
+        BYHIP_GEMV_CASE(false, true, true)
+        BYHIP_GEMV_CASE(false, false, true)
+        BYHIP_GEMV_CASE(true, true, false)
+        BYHIP_GEMV_CASE(true, false, false)
+        BYHIP_GEMV_CASE(false, true, false)
+        BYHIP_GEMV_CASE(false, false, false)
+#undef BYHIP_GEMV_CASE
+    }
+}
+
+template <int M, bool XF32>
+void launch_cpl(int cpl, const GemvArgs& a, const byhip_q4w* w, bool blk, int y_dtype) {
+    switch (cpl) {
+    case 1: launch_szb<M, 1, XF32>(a, w, blk, y_dtype); break;
+    case 2: launch_szb<M, 2, XF32>(a, w, blk, y_dtype); break;
+    case 4: launch_szb<M, 4, XF32>(a, w, blk, y_dtype); break;
+    default: launch_szb<M, 8, XF32>(a, w, blk, y_dtype); break;
+    }
+}
+
+// Chunks of 32 values per lane the GEMV keeps in registers for K (a power of two up to 8).
+int gemv_cpl(int K) {
+    const int G = K / 32;
+    int cpl = 1;
+    while (cpl * kWave < G) cpl *= 2;
+    return cpl;
+}
+
+}  // namespace
+
+bool q4_gemv_eligible(const byhip_q4w* w, int M, int x_dtype) {
+    if (w->K % 32 != 0 || (w->group != 0 && w->group % 32 != 0)) return false;
+    const int xs = x_dtype == BYHIP_F32 ? 2 : 1;
+    const int cpl = gemv_cpl(w->K);
+    const int m = std::min(M, 4);
+    // 32-bit buffer offsets (below the out-of-range marker) for weights, scales and activations
+    const uint64_t lim = kOutOfRange - 64;
+    const bool fits = (uint64_t)w->N * w->row_bytes < lim && (uint64_t)(w->N + 8) * (w->K / 32 + w->gpr) * 4 < lim &&
+                      (uint64_t)m * w->K * 4 < lim;
+    const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0;
+    return fits && aligned && cpl <= 8 && m * xs * cpl <= 8;
+}
+
+void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
+    const int cpl = gemv_cpl(w->K);
+    const size_t xb = dtype_bytes(x_dtype), yb = dtype_bytes(y_dtype);
+    const bool blk = w->sblk != nullptr;
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        const int mm = std::min(4, M - m0);
+        GemvArgs a;
+        a.x = static_cast<const uint8_t*>(x) + (size_t)m0 * w->K * xb;
+        a.wq = w->wq;
+        a.scales = blk ? w->sblk : w->scales;
+        a.zeros = blk ? w->zblk : w->zeros;
+        a.zero_value = w->zero_value;
+        a.y = static_cast<uint8_t*>(y) + (size_t)m0 * w->N * yb;
+        a.K = w->K; a.N = w->N; a.gpr = w->gpr; a.row_bytes = (int)w->row_bytes;
+        a.group_chunks = w->group / 32;
+        a.n_pad = (w->N + 7) / 8 * 8;
+        if (x_dtype == BYHIP_F32) {
+            switch (mm) {
+            case 1: launch_cpl<1, true>(cpl, a, w, blk, y_dtype); break;
+            case 2: launch_cpl<2, true>(cpl, a, w, blk, y_dtype); break;
+            case 3: launch_cpl<3, true>(cpl, a, w, blk, y_dtype); break;
+            default: launch_cpl<4, true>(cpl, a, w, blk, y_dtype); break;
+            }
+        } else {
+            switch (mm) {
+            case 1: launch_cpl<1, false>(cpl, a, w, blk, y_dtype); break;
+            case 2: launch_cpl<2, false>(cpl, a, w, blk, y_dtype); break;
+            case 3: launch_cpl<3, false>(cpl, a, w, blk, y_dtype); break;
+            default: launch_cpl<4, false>(cpl, a, w, blk, y_dtype); break;
+            }
+        }
+    }
+}
+
+}  // namespace byhip

@@ -35,6 +35,9 @@ void set_error(const std::string& msg);
 
 // Every entry point: injected fault first, then the device must be initialised.
 void enter_compute();
+// Entry points that wait for the device or write memory outside a kernel call this first: they
+// cannot be part of a recorded session (stream capture).
+void no_host_sync(const char* what);
 hipStream_t stream();
 int compute_units();
 
@@ -87,4 +90,11 @@ struct byhip_q4w {
     int zero_uniform;
     float zero_value;
     size_t bytes;               // device bytes held
+    // Decode copy of the scales (and non-uniform zeros) per 32-value chunk in blocks of 8 rows,
+    // [ceil(N/8)][K/32][8] (fp16 scales when scale_f16, fp32 zeros), so one 16-byte load gives a
+    // lane the scales of 8 consecutive rows. Present when K and the group are multiples of 32
+    // (or the group is 0); null otherwise.
+    void* sblk = nullptr;
+    float* zblk = nullptr;
+    int blk_scale_f16 = 0;
 };

@@ -28,6 +28,64 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP lane exchange within rows of 16 lanes (row_shr / quad_perm / mirror controls).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_rows(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave, all in DPP: rows of 16 lanes first (quad swaps, half-row and row
+// mirrors), then row_bcast:15 adds row 0 into row 1 and row 2 into row 3, and row_bcast:31 adds
+// rows 0-1 into rows 2-3. The total is valid in lane 63.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v += dpp<0xB1>(v);           // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);           // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);          // row_half_mirror
+    v += dpp<0x140>(v);          // row_mirror
+    v += dpp_rows<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_rows<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Sum over the 64 lanes of a wave; the total is valid in lane 0 only. Within each row of 16 lanes
+// the sum is formed with DPP (quad_perm swaps, then half-row and row mirrors), then the four row
+// sums are read from lanes 0, 16, 32, 48.
+__device__ __forceinline__ float wave_sum_lane0(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Buffer resource over `bytes` bytes at `p`: raw buffer loads take 32-bit offsets and return 0 for
+// any offset past the end (hardware range check), so edge tiles need no clamps.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;  // an offset every resource rejects
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t off) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load2(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
 // binary32 -> bfloat16 bits, round to nearest even; NaN stays NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     uint32_t u = __builtin_bit_cast(uint32_t, f);

@@ -5,6 +5,7 @@
 // check, frees deferred while a session is open, GPU time from events around each session.
 #include "byhip_internal.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -34,6 +35,10 @@ struct State {
     bool timing = false;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     double gpu_seconds = 0.0;
+    // record / replay (sessionBeginRecording .. sessionFreeRecording, gpubackend.nim:2502-2552)
+    bool recording = false;
+    std::vector<hipGraphExec_t> recordings;  // id -> executable graph (null once freed)
+    int last_recording = -1;
 };
 
 State& st() {
@@ -85,6 +90,11 @@ void enter_compute() {
 
 hipStream_t stream() { return st().stream; }
 int compute_units() { return st().prop.multiProcessorCount; }
+
+void no_host_sync(const char* what) {
+    if (st().recording)
+        fail("byhip: %s waits for the device and is not allowed while a session is recorded", what);
+}
 
 size_t alloc_bytes(const void* p) {
     State& s = st();
@@ -145,6 +155,7 @@ void read_small(const void* p, size_t off, void* dst, size_t bytes) {
             return;
         }
     }
+    no_host_sync("reading a device buffer");
     BYHIP_HIP(hipStreamSynchronize(stream()));
     BYHIP_HIP(hipMemcpy(dst, static_cast<const uint8_t*>(p) + off, bytes, hipMemcpyDeviceToHost));
 }
@@ -218,6 +229,7 @@ int byhip_alloc(size_t bytes, void** dptr) {
 int byhip_free(void* dptr) {
     return guard([&] {
         enter_compute();
+        no_host_sync("byhip_free");
         BYHIP_HIP(hipStreamSynchronize(stream()));
         device_free(dptr);
     });
@@ -226,6 +238,7 @@ int byhip_free(void* dptr) {
 int byhip_upload(void* dptr, size_t dst_off, const void* src, size_t bytes) {
     return guard([&] {
         enter_compute();
+        no_host_sync("byhip_upload");
         if (!bytes) return;
         if (!src) fail("byhip: null upload source");
         check_span(static_cast<uint8_t*>(dptr) + dst_off, bytes, "upload destination");
@@ -250,6 +263,7 @@ int byhip_upload(void* dptr, size_t dst_off, const void* src, size_t bytes) {
 int byhip_read(const void* dptr, size_t src_off, void* dst, size_t bytes) {
     return guard([&] {
         enter_compute();
+        no_host_sync("byhip_read");
         if (!bytes) return;
         if (!dst) fail("byhip: null read destination");
         check_span(static_cast<const uint8_t*>(dptr) + src_off, bytes, "read source");
@@ -262,6 +276,7 @@ int byhip_read(const void* dptr, size_t src_off, void* dst, size_t bytes) {
 int byhip_memset(void* dptr, int value, size_t bytes) {
     return guard([&] {
         enter_compute();
+        no_host_sync("byhip_memset");
         if (!bytes) return;
         check_span(dptr, bytes, "memset destination");
         BYHIP_HIP(hipMemsetAsync(dptr, value, bytes, stream()));
@@ -275,6 +290,7 @@ int byhip_memset(void* dptr, int value, size_t bytes) {
 int byhip_synchronize(void) {
     return guard([&] {
         enter_compute();
+        no_host_sync("byhip_synchronize");
         BYHIP_HIP(hipStreamSynchronize(stream()));
     });
 }
@@ -314,6 +330,7 @@ static void* session_new_buffer(const void* data, size_t bytes, bool zero) {
 int byhip_session_upload(const float* data, size_t n, void** out) {
     return guard([&] {
         enter_compute();
+        no_host_sync("sessionUpload");
         if (!out) fail("byhip: null output handle");
         if (n && !data) fail("byhip: null upload data");
         *out = session_new_buffer(data, n * sizeof(float), false);
@@ -323,6 +340,7 @@ int byhip_session_upload(const float* data, size_t n, void** out) {
 int byhip_session_upload_bytes(const void* data, size_t bytes, void** out) {
     return guard([&] {
         enter_compute();
+        no_host_sync("sessionUpload");
         if (!out) fail("byhip: null output handle");
         if (bytes && !data) fail("byhip: null upload data");
         *out = session_new_buffer(data, bytes, false);
@@ -332,9 +350,42 @@ int byhip_session_upload_bytes(const void* data, size_t bytes, void** out) {
 int byhip_session_alloc_scratch(size_t n, void** out) {
     return guard([&] {
         enter_compute();
+        no_host_sync("sessionAllocScratch");
         if (!out) fail("byhip: null output handle");
         *out = session_new_buffer(nullptr, n * sizeof(float), true);
     });
+}
+
+// Ends a recorded session: the captured work becomes an executable graph, which is launched once
+// (the session's work happens, as a kept Vulkan command buffer is also submitted) and kept.
+static void end_recording(State& s) {
+    hipGraph_t graph = nullptr;
+    s.recording = false;
+    s.session_open = false;
+    hipError_t e = hipStreamEndCapture(s.stream, &graph);
+    if (e != hipSuccess || !graph) {
+        (void)hipGetLastError();
+        fail("byhip: the recorded session could not be kept: %s", hipGetErrorString(e));
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) fail("byhip: instantiating the recorded session failed: %s", hipGetErrorString(e));
+    s.recordings.push_back(exec);
+    s.last_recording = (int)s.recordings.size() - 1;
+    if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+    BYHIP_HIP(hipGraphLaunch(exec, s.stream));
+    if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+    e = hipStreamSynchronize(s.stream);
+    std::vector<void*> frees;
+    frees.swap(s.deferred_frees);
+    if (e != hipSuccess) fail("byhip: session failed on the device: %s", hipGetErrorString(e));
+    if (s.timing) {
+        float ms = 0.0f;
+        BYHIP_HIP(hipEventElapsedTime(&ms, s.ev_begin, s.ev_end));
+        s.gpu_seconds += ms * 1e-3;
+    }
+    for (void* p : frees) device_free(p);
 }
 
 int byhip_session_end(void) {
@@ -343,6 +394,11 @@ int byhip_session_end(void) {
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (!s.session_open) fail("byhip: no session is open");
+        if (s.recording) {
+            end_recording(s);
+            return;
+        }
+        s.last_recording = -1;
         if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
         hipError_t e = hipStreamSynchronize(s.stream);
         s.session_open = false;
@@ -371,6 +427,12 @@ int byhip_session_recover(void) {
         enter_compute();
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.recording) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(s.stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            s.recording = false;
+        }
         (void)hipStreamSynchronize(s.stream);
         (void)hipGetLastError();
         s.session_open = false;
@@ -411,4 +473,79 @@ int byhip_session_set_gpu_timing(int on) {
 
 double byhip_session_gpu_seconds(void) { return st().gpu_seconds; }
 
+int byhip_session_can_record(void) { return 1; }
+
+int byhip_session_begin_recording(void) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) fail("byhip: a session is already open");
+        BYHIP_HIP(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+        s.session_open = true;
+        s.recording = true;
+    });
+}
+
+int byhip_session_last_recording(void) { return st().last_recording; }
+
+int byhip_session_replay(int id, int times) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) fail("byhip: replay runs outside a session");
+        if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id])
+            fail("byhip: no recording %d", id);
+        if (times < 1) fail("byhip: replay count %d", times);
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+        for (int i = 0; i < times; ++i) BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        BYHIP_HIP(hipStreamSynchronize(s.stream));
+        if (s.timing) {
+            float ms = 0.0f;
+            BYHIP_HIP(hipEventElapsedTime(&ms, s.ev_begin, s.ev_end));
+            s.gpu_seconds += ms * 1e-3;
+        }
+    });
+}
+
+int byhip_session_free_recording(int id) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id]) return;
+        BYHIP_HIP(hipStreamSynchronize(s.stream));
+        BYHIP_HIP(hipGraphExecDestroy(s.recordings[id]));
+        s.recordings[id] = nullptr;
+    });
+}
+
 }  // extern "C"
+
+// ── A plain copy kernel (bandwidth and HBM-counter calibration) ─────────────────────────────
+
+namespace {
+__global__ __launch_bounds__(256) void copy_words(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                  size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+}  // namespace
+
+extern "C" int byhip_debug_copy(void* dst, const void* src, size_t bytes) {
+    return guard([&] {
+        enter_compute();
+        if (bytes % 16 || reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+            fail("byhip: copy needs 16-byte aligned pointers and sizes");
+        check_span(dst, bytes, "copy destination");
+        check_span(src, bytes, "copy source");
+        const size_t n = bytes / 16;
+        const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, (size_t)compute_units() * 16);
+        if (n == 0) return;
+        hipLaunchKernelGGL(copy_words, dim3(grid), dim3(256), 0, stream(), static_cast<const uint4*>(src),
+                           static_cast<uint4*>(dst), n);
+        BYHIP_LAUNCHED("copy_words");
+    });
+}

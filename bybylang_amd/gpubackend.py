@@ -175,6 +175,35 @@ def sessionGpuSeconds(backend: GpuBackend) -> float:
     return float(load().byhip_session_gpu_seconds())
 
 
+# ── record / replay (gpubackend.nim:2502-2552), kept as HIP graphs ──────────────────────────
+
+
+def sessionCanRecord(backend: GpuBackend) -> bool:
+    _require_hip(backend)
+    return load().byhip_session_can_record() == 1
+
+
+def sessionBeginRecording(backend: GpuBackend) -> bool:
+    _require_hip(backend)
+    return ensureGpuInit(backend) and load().byhip_session_begin_recording() == _abi.BYHIP_OK
+
+
+def sessionLastRecording(backend: GpuBackend) -> int:
+    _require_hip(backend)
+    return int(load().byhip_session_last_recording())
+
+
+def sessionReplay(backend: GpuBackend, id: int, times: int = 1) -> bool:
+    """Submits a kept recording again (`times` back to back) and waits for it."""
+    _require_hip(backend)
+    return load().byhip_session_replay(int(id), int(times)) == _abi.BYHIP_OK
+
+
+def sessionFreeRecording(backend: GpuBackend, id: int) -> None:
+    _require_hip(backend)
+    load().byhip_session_free_recording(int(id))
+
+
 # ── resident Q4 weights and Q4 ops ──────────────────────────────────────────────────────────
 
 

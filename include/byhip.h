@@ -115,6 +115,21 @@ int byhip_session_free(void* h);
 int byhip_session_set_gpu_timing(int on);
 double byhip_session_gpu_seconds(void);
 
+/* Record / replay as HIP graphs (gpubackend.nim:2502-2552, vulkan_driver.nim:1659-2030).
+ * sessionCanRecord: always 1 on this backend. */
+int byhip_session_can_record(void);
+/* sessionBeginRecording: opens a session whose queued work is captured; it must be
+ * self-contained (entry points that wait for the device, upload or clear memory fail while
+ * recording). byhip_session_end() keeps it as a graph, runs it once and waits. */
+int byhip_session_begin_recording(void);
+/* sessionLastRecording: id kept by the last byhip_session_end(), or -1. */
+int byhip_session_last_recording(void);
+/* sessionReplay: launches recording `id` `times` times back to back (outside a session), then
+ * waits; counted by byhip_session_gpu_seconds() when timing is on. */
+int byhip_session_replay(int id, int times);
+/* sessionFreeRecording. */
+int byhip_session_free_recording(int id);
+
 /* ── Q4 block-dequant GEMV / GEMM ─────────────────────────────────────────────────────────── */
 
 /* Resident Q4 weights: the ResidentWeightHandle of gpubackend.nim:2813-2825. */
@@ -202,6 +217,9 @@ int byhip_debug_unpack_q4(const byhip_q4w* w, uint8_t* codes, float* scales, flo
  * [N*K] = lut[code] * lut[16 + scale byte] as fp32. */
 int byhip_debug_unpack_fp4km(const uint8_t* blob, size_t scale_base, const float* lut,
                              size_t lut_base, int K, int N, uint8_t* codes, float* weights);
+/* A plain device copy of `bytes` (16-byte multiples): the reference point for HBM bandwidth and
+ * for scaling hardware traffic counters. No counterpart in the reference. */
+int byhip_debug_copy(void* dst, const void* src, size_t bytes);
 
 #ifdef __cplusplus
 }
