@@ -11,6 +11,12 @@ the weights (529 MB, more than twice the 256 MB Infinity Cache, so the reads com
 timed with HIP events on the library stream. The other configurations (prefill Q4 GEMM, MXFP4
 GEMM, the decoder-layer batch) are reported under "configs" with the same method.
 
+roofline.traffic: HBM bytes per launch of the GEMV, read from profiles/q4_gemv_c1_traffic.json,
+which bybylang_amd.profile_summary writes from two rocprofv3 --pmc runs of this script
+(FETCH_SIZE, WRITE_SIZE) with --copy-probe, each counter scaled by what it reads for the
+library's copy kernel moving a known number of bytes in the same run; null when that file is
+absent.
+
 cpu_baseline: the reference's own CPU path for this op (nimf_cpu_matmul_q4,
 backends/cpu/cpu_kernels_impl.inc:293-319, compiled from its sources into oracle/_ref), single
 threaded as the reference runs, timed on full config-1 passes for about ten seconds; when that
@@ -219,6 +225,35 @@ def cpu_baseline(seconds: float = 10.0):
                       f"{platform.processor() or platform.machine()}"}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_c1_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return int(round(t["traffic_bytes"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_probe(mib: int, times: int = 10):
+    """Runs the library's copy kernel on `mib` MiB device to device `times` times: the known
+    transfer that a counter run scales FETCH_SIZE / WRITE_SIZE by."""
+    from bybylang_amd import _abi
+    from bybylang_amd import device as dev
+    n = mib << 20
+    src, dst = dev.DeviceBuffer(n), dev.DeviceBuffer(n)
+    lib = _abi.load()
+    for _ in range(times):
+        _abi.check(lib.byhip_debug_copy(dst.ptr, src.ptr, n))
+    dev.synchronize()
+    src.close()
+    dst.close()
+    return n
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -227,6 +262,8 @@ def main() -> int:
     ap.add_argument("--configs", default="c1,c2,c3,c4",
                     help="configurations to measure (c1 is the headline and always runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run the copy kernel on MIB MiB (calibration for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.stderr.write("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -241,6 +278,7 @@ def main() -> int:
     dev.init(0)
     info = dev.device_info()
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
+    probe = copy_probe(args.copy_probe) if args.copy_probe > 0 else 0
 
     c1 = bench_c1(dev, synth, args.steps, args.warmup)
     configs = {}
@@ -274,11 +312,13 @@ def main() -> int:
                    "compute_units": info.get("compute_units")},
         "roofline": {"bound": "hbm", "achieved": round(c1["GBps"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(c1["GBps"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "q4_gemv_dot2",
+                     "traffic": measured_traffic(), "kernel": "q4_gemv",
                      "bytes_per_launch": c1["bytes_per_step"], "avg_launch_us": round(c1["us_per_step"], 3)},
         "cpu_baseline": cpu,
         "configs": configs,
     }
+    if probe:
+        line["copy_probe_bytes"] = probe
     print(json.dumps(line))
     return 0
 

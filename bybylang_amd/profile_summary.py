@@ -1,0 +1,95 @@
+"""Summaries of rocprofv3 result databases for the committed profiles.
+
+    python -m bybylang_amd.profile_summary trace DB
+        per-kernel dispatch count and average / min / max duration (kernel-trace runs)
+
+    python -m bybylang_amd.profile_summary traffic --fetch DB --write DB --copy-bytes N
+                                                   --kernel SUBSTRING [--json OUT]
+        HBM bytes per dispatch of the kernel whose name contains SUBSTRING, from a FETCH_SIZE run
+        and a WRITE_SIZE run (KiB per dispatch). Each counter is scaled by what it reads for the
+        library's copy kernel (copy_words) moving N bytes in the same run, so the figure is in the
+        units of a known transfer: factor = N / (counter KiB * 1024) for reads and for writes.
+
+The databases are the *_results.db files rocprofv3 writes with -d/-o.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import json
+import sqlite3
+import sys
+
+
+def kernel_durations(db: str):
+    con = sqlite3.connect(db)
+    rows = con.execute("select name, count(*), avg(end-start), min(end-start), max(end-start) "
+                       "from kernels group by name order by sum(end-start) desc").fetchall()
+    con.close()
+    return rows
+
+
+def counter_per_dispatch(db: str, counter: str):
+    """{kernel name: [value summed over counter instances, per dispatch]}"""
+    con = sqlite3.connect(db)
+    rows = con.execute("select dispatch_id, kernel_name, value from counters_collection "
+                       "where counter_name = ?", (counter,)).fetchall()
+    con.close()
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    for d, k, v in rows:
+        per[k][d] += v
+    return {k: list(v.values()) for k, v in per.items()}
+
+
+def _pick(per: dict, substring: str):
+    names = [k for k in per if substring in k]
+    if len(names) != 1:
+        raise SystemExit(f"expected one kernel matching {substring!r}, found {names}")
+    vals = per[names[0]]
+    return names[0], sum(vals) / len(vals), len(vals)
+
+
+def traffic(fetch_db: str, write_db: str, copy_bytes: int, kernel: str) -> dict:
+    fetch = counter_per_dispatch(fetch_db, "FETCH_SIZE")
+    write = counter_per_dispatch(write_db, "WRITE_SIZE")
+    _, copy_f, ncf = _pick(fetch, "copy_words")
+    _, copy_w, ncw = _pick(write, "copy_words")
+    name, kf, nkf = _pick(fetch, kernel)
+    _, kw, nkw = _pick(write, kernel)
+    ff = copy_bytes / (copy_f * 1024.0)
+    fw = copy_bytes / (copy_w * 1024.0)
+    return {"kernel": name, "dispatches": {"fetch": nkf, "write": nkw, "copy": [ncf, ncw]},
+            "copy_bytes": copy_bytes, "copy_fetch_kib": copy_f, "copy_write_kib": copy_w,
+            "fetch_factor": ff, "write_factor": fw,
+            "kernel_fetch_kib": kf, "kernel_write_kib": kw,
+            "fetch_bytes": kf * 1024.0 * ff, "write_bytes": kw * 1024.0 * fw,
+            "traffic_bytes": kf * 1024.0 * ff + kw * 1024.0 * fw}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("db")
+    r = sub.add_parser("traffic")
+    r.add_argument("--fetch", required=True)
+    r.add_argument("--write", required=True)
+    r.add_argument("--copy-bytes", type=int, required=True)
+    r.add_argument("--kernel", required=True)
+    r.add_argument("--json")
+    a = ap.parse_args(argv)
+    if a.cmd == "trace":
+        print(f"| kernel | dispatches | avg us | min us | max us |\n|---|---:|---:|---:|---:|")
+        for name, n, avg, mn, mx in kernel_durations(a.db):
+            print(f"| `{name[:110]}` | {n} | {avg / 1e3:.3f} | {mn / 1e3:.3f} | {mx / 1e3:.3f} |")
+        return 0
+    res = traffic(a.fetch, a.write, a.copy_bytes, a.kernel)
+    print(json.dumps(res, indent=1))
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(res, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
