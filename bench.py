@@ -6,8 +6,8 @@
 Prints ONE JSON line. The headline (`value`) is config 1 of BASELINE.json: the decode Q4 GEMV
 (M=1, K=4096, N=14336, block-32 Q4 weights with fp16 scales, fp16 x and y, fp32 accumulation) in
 GB/s of algorithmic bytes, inputs resident in HBM. A step is one GEMV launch; K launches are
-recorded as one HIP graph (the session record / replay route) cycling through 16 resident copies of
-the weights (529 MB, more than twice the 256 MB Infinity Cache, so the reads come from HBM), and
+recorded as one HIP graph (the session record / replay route) cycling through 17 resident copies of
+the weights (562 MB, more than twice the 256 MB Infinity Cache, so the reads come from HBM), and
 timed with HIP events on the library stream. The other configurations (prefill Q4 GEMM, MXFP4
 GEMM, the decoder-layer batch) are reported under "configs" with the same method.
 
