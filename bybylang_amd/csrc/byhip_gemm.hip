@@ -251,6 +251,223 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
         }
 }
 
+// Pipelined Q4 GEMM for the benchmark format: fp16 activations, fp16 scales, one integral zero,
+// group 0 or 32 * 2^j, K % 64 == 0. A 256-thread block computes a BM x BN tile (BM 32 or 64, BN 64
+// or 128, chosen per shape) in K steps of 64 (two 32-value groups); its four waves each own a
+// 32-row slice of BN / (4 / (BM / 32)) columns, as 16 x 16 fragments of v_mfma_f32_16x16x32_f16.
+// LDS holds two steps (double buffer, one barrier per step); each thread's global loads run three
+// steps ahead in registers (three register sets rotate), so a step's MFMAs overlap the
+// dequantization of the next step and the loads of later ones.
+//   x: each thread stages BM / 4 values of one row, permuted to the weights' (k, k+4) pair order.
+//   W: each thread dequantizes BN / 4 values of one column. A nibble at bits 0-3 of a half ORed
+//      into 0x6400 is the fp16 1024 + q, at bits 4-7 into 0x5400 it is 64 + q; minus 1024 + z or
+//      64 + z that is q - z exactly, times the fp16 scale (one rounding), as Q4Fast does.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+constexpr int PBK = 64;
+constexpr int PLD = PBK + 8;  // halves per LDS row (16-byte pad: conflict-free operand reads)
+
+template <int BM, int BN>
+struct PipeShape {
+    static constexpr int WGM = BM / 32, WGN = 4 / WGM;   // wave grid
+    static constexpr int WN = BN / WGN, FN = WN / 16;     // columns and fragments per wave
+    static constexpr int XV = BM / 4;                     // activations staged per thread (8 or 16)
+    static constexpr int XT = PBK / XV;                   // threads per activation row
+    static constexpr int WV = BN / 4;                     // weights dequantized per thread (16 or 32)
+    static constexpr int WT = PBK / WV;                   // threads per weight column
+    static_assert(WGM * WGN == 4 && FN >= 1, "tile shape");
+};
+
+struct PipeRegs {
+    uint4 x0, x1;  // up to 16 activations of one row
+    uint4 w;       // up to 32 nibbles of one column
+    uint32_t s;    // their fp16 scale
+};
+
+// (a.lo, b.lo) and (a.hi, b.hi) halves of two dwords.
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+// 8 activations (x0..x7) reordered to (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+__device__ __forceinline__ uint4 perm8(uint4 v) {
+    return make_uint4(pair_lo(v.x, v.z), pair_hi(v.x, v.z), pair_lo(v.y, v.w), pair_hi(v.y, v.w));
+}
+
+template <int BM, int BN, int YT>
+__global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
+    using S = PipeShape<BM, BN>;
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * PLD];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * PLD];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid / S::WGN, wn = wid % S::WGN;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int K = a.K, nsteps = K / PBK;
+
+    // Rows past M / N read zeros through the buffer range checks (offsets stay below 2^32: the
+    // launcher checks the sizes).
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
+    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
+    const rsrc_t sr = make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
+    const int arow = tid / S::XT, aseg = tid % S::XT;    // values aseg*XV .. +XV-1 of the step
+    const int bcol = tid / S::WT, bseg = tid % S::WT;    // values bseg*WV .. +WV-1 of the step
+    const uint32_t xoff = (uint32_t)(m0 + arow) * (uint32_t)K * 2u + (uint32_t)(2 * S::XV * aseg);
+    const uint32_t woff = (uint32_t)(n0 + bcol) * (uint32_t)a.row_bytes + (uint32_t)(S::WV / 2 * bseg);
+    const uint32_t soff = (uint32_t)(n0 + bcol) * (uint32_t)a.gpr;
+    const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;  // group: 0 or 32 * 2^j
+
+    auto gload = [&](PipeRegs& r, int s) {
+        const int k0 = min(s, nsteps - 1) * PBK;
+        const v4u u0 = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 2u * k0, 0, 0);
+        r.x0 = make_uint4(u0[0], u0[1], u0[2], u0[3]);
+        if constexpr (S::XV == 16) {
+            const v4u u1 = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 2u * k0 + 16u, 0, 0);
+            r.x1 = make_uint4(u1[0], u1[1], u1[2], u1[3]);
+        }
+        if constexpr (S::WV == 32) {
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wr, woff + (uint32_t)(k0 >> 1), 0, 0);
+            r.w = make_uint4(v[0], v[1], v[2], v[3]);
+        } else {
+            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(wr, woff + (uint32_t)(k0 >> 1), 0, 0);
+            r.w = make_uint4(v[0], v[1], 0u, 0u);
+        }
+        const int g = a.group ? ((k0 + bseg * S::WV) >> 5) >> gshift : 0;
+        r.s = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (soff + (uint32_t)g), 0, 0);
+    };
+    const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
+    const h2 zz_lo = {zlo, zlo}, zz_hi = {zhi, zhi};
+    // The magic words live in VGPRs so each AND-OR is one v_and_or_b32.
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
+    auto stage = [&](const PipeRegs& r, int buf) {
+        uint4* da = reinterpret_cast<uint4*>(&As[buf][arow * PLD + S::XV * aseg]);
+        da[0] = perm8(r.x0);
+        if constexpr (S::XV == 16) da[1] = perm8(r.x1);
+        // weights: word d holds values k..k+7; pair i = (k+i, k+i+4)
+        const _Float16 sc = bits_h((uint16_t)r.s);
+        const h2 ss = {sc, sc};
+        const uint32_t dw[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+        uint4* db = reinterpret_cast<uint4*>(&Bs[buf][bcol * PLD + S::WV * bseg]);
+#pragma unroll
+        for (int w = 0; w < S::WV / 8; ++w) {
+            const uint32_t d8 = dw[w] >> 8;
+            const h2 q0 = bits_h2((dw[w] & 0x000F000Fu) | mag_lo);
+            const h2 q1 = bits_h2((dw[w] & 0x00F000F0u) | mag_hi);
+            const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
+            const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
+            db[w] = make_uint4(h2_bits((q0 - zz_lo) * ss), h2_bits((q1 - zz_hi) * ss),
+                               h2_bits((q2 - zz_lo) * ss), h2_bits((q3 - zz_hi) * ss));
+        }
+    };
+
+    f4 acc[2][S::FN];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < S::FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int kc = 8 * (lane >> 4);
+    auto mma = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < PBK; kk += 32) {
+            h8 av[2], bv[S::FN];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                av[i] = *reinterpret_cast<const h8*>(&As[buf][(wm * 32 + i * 16 + (lane & 15)) * PLD + kk + kc]);
+#pragma unroll
+            for (int j = 0; j < S::FN; ++j)
+                bv[j] = *reinterpret_cast<const h8*>(&Bs[buf][(wn * S::WN + j * 16 + (lane & 15)) * PLD + kk + kc]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < S::FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    PipeRegs r0, r1, r2;
+    gload(r0, 0);
+    gload(r1, 1);
+    gload(r2, 2);
+    stage(r0, 0);
+    __syncthreads();
+    // Step s: MFMAs on buffer s % 2; stage step s + 1 (registers loaded three steps ago) into the
+    // other buffer; load step s + 3 into the registers step s used.
+    auto step = [&](int s, PipeRegs& rs, PipeRegs& rn, bool more) {
+        mma(s & 1);
+        // Keeps each accumulator in its AGPRs across steps (otherwise the allocator rotates them
+        // through copies at the loop head).
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < S::FN; ++j) asm volatile("" : "+a"(acc[i][j]));
+        if (more) stage(rn, (s + 1) & 1);
+        gload(rs, s + 3);
+        __syncthreads();
+    };
+    int s = 0;
+    for (; s + 3 < nsteps; s += 3) {  // every step here has a successor
+        step(s, r0, r1, true);
+        step(s + 1, r1, r2, true);
+        step(s + 2, r2, r0, true);
+    }
+    if (s < nsteps) step(s, r0, r1, s + 1 < nsteps);
+    if (s + 1 < nsteps) step(s + 1, r1, r2, s + 2 < nsteps);
+    if (s + 2 < nsteps) step(s + 2, r2, r0, false);
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < S::FN; ++j) {
+            const int n = n0 + wn * S::WN + j * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                if (m < a.M && n < a.N) store_y<YT>(a.y, (size_t)m * a.N + n, acc[i][j][r]);
+            }
+        }
+}
+
+// Whether the pipelined Q4 kernel takes these arguments.
+bool q4_pipe_ok(const GemmArgs& a) {
+    const bool pow2_group = a.group % 32 == 0 && ((a.group >> 5) & ((a.group >> 5) - 1)) == 0;
+    return a.x_dtype == BYHIP_F16 && a.K % PBK == 0 && a.scale_f16 && !a.zeros &&
+           (a.group == 0 || pow2_group) && a.row_bytes % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && reinterpret_cast<uintptr_t>(a.wq) % 16 == 0 &&
+           (uint64_t)(a.M + 64) * a.K * 2 < kOutOfRange && (uint64_t)(a.N + 128) * a.row_bytes < kOutOfRange &&
+           (uint64_t)(a.N + 128) * a.gpr * 2 < kOutOfRange;
+}
+
+template <int BM, int BN>
+void launch_q4_pipe_shape(const GemmArgs& a) {
+    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+    switch (a.y_dtype) {
+    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
+    default: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_BF16>), grid, dim3(256), 0, stream(), a); break;
+    }
+    BYHIP_LAUNCHED("q4_gemm_pipe");
+}
+
+// Tile choice: 64 x 128 when that gives at least one block per CU, else 64 x 64; 32-row tiles when
+// M <= 32 (32 x 128 if that fills the chip, else 32 x 64). BYHIP_Q4_TILE=1..4 forces 64x128,
+// 64x64, 32x128, 32x64.
+void launch_q4_pipe(const GemmArgs& a) {
+    const long cus = compute_units();
+    auto blocks = [&](int bm, int bn) { return (long)((a.N + bn - 1) / bn) * ((a.M + bm - 1) / bm); };
+    int tile = env_int("BYHIP_Q4_TILE", 0);
+    if (tile < 1 || tile > 4) {
+        if (a.M <= 32) tile = blocks(32, 128) >= cus ? 3 : 4;
+        else tile = blocks(64, 128) >= cus ? 1 : 2;
+    }
+    switch (tile) {
+    case 1: launch_q4_pipe_shape<64, 128>(a); break;
+    case 2: launch_q4_pipe_shape<64, 64>(a); break;
+    case 3: launch_q4_pipe_shape<32, 128>(a); break;
+    default: launch_q4_pipe_shape<32, 64>(a); break;
+    }
+}
+
 template <BFormat F, bool XF32>
 void launch_fx(const GemmArgs& a) {
     const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
@@ -281,7 +498,10 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0) return;
     if (a.M > 65535 * BM) fail("byhip: M=%d too large for one launch", a.M);
     switch (fmt) {
-    case BFormat::Q4Fast: launch_f<BFormat::Q4Fast>(a); break;
+    case BFormat::Q4Fast:
+        if (q4_pipe_ok(a)) launch_q4_pipe(a);
+        else launch_f<BFormat::Q4Fast>(a);
+        break;
     case BFormat::Q4Generic: launch_f<BFormat::Q4Generic>(a); break;
     case BFormat::Fp4Km: launch_f<BFormat::Fp4Km>(a); break;
     case BFormat::F16: launch_f<BFormat::F16>(a); break;

@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -67,6 +68,12 @@ int guard(F&& f) {
         set_error("byhip: unknown exception");
         return BYHIP_ERROR;
     }
+}
+
+// Integer value of environment variable `name` (tuning overrides), or dflt when unset or empty.
+inline int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
 }
 
 inline size_t dtype_bytes(int dt) {

@@ -201,11 +201,6 @@ byhip_q4w* build_resident(const uint8_t* wq_rows, const float* scales, const flo
     return w;
 }
 
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
-
 template <bool XF32, bool SF16, bool ZU>
 void launch_generic_y(const void* x, const byhip_q4w* w, void* y, int y_dtype, int M) {
     const int grid = (w->N + 3) / 4;

@@ -129,6 +129,24 @@ def test_q4_dtypes_and_rows(hip, oracle, M, x_dtype, y_dtype):
         tier_check(got, want, TIER_F32_ACC)
 
 
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("shape", [(64, 512, 256), (130, 256, 200), (24, 640, 136), (33, 128, 64)])
+def test_q4_gemm_tiles(hip, oracle, monkeypatch, tile, shape):
+    """Every tile shape of the pipelined Q4 GEMM (64x128, 64x64, 32x128, 32x64, forced through
+    BYHIP_Q4_TILE), on ragged M and N and short K, fp16 in and out, against the oracle."""
+    from bybylang_amd import synth
+    M, K, N = shape
+    monkeypatch.setenv("BYHIP_Q4_TILE", str(tile))
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    g = synth.rng(7000 + 17 * M + N)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 pipe tile={tile} M={M} K={K} N={N}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, hip.F16)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
 @pytest.mark.parametrize("case", ["group0", "group64", "group128", "asym_zero", "int_zero5",
                                   "f32_scales", "odd_k", "gpr_pad", "k32"])
 @pytest.mark.parametrize("M", [1, 3, 24])
