@@ -35,6 +35,10 @@ struct GemmArgs {
     const float* lut = nullptr;    // the 272 floats (16 values, 256 scales)
     // F16
     const uint16_t* w16 = nullptr;
+    // Split-K (set by the launcher): block z of the grid covers K steps [z * split_steps, ...) and
+    // writes fp32 partial sums to part[z][M][N]; a second kernel adds them in z order into y.
+    float* part = nullptr;
+    int split_steps = 0;
 };
 
 // Queues the GEMM on the library stream; K % 32 == 0 is required (callers check).

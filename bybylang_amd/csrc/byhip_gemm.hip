@@ -16,6 +16,8 @@
 //   others  natural order.
 // fp32 activations are split into hi = fp16(x) and lo = fp16(x - hi) and multiplied twice, which
 // keeps ~22 bits of x; fp16 activations are used as they are.
+#include <algorithm>
+
 #include "byhip_gemm.h"
 #include "byhip_internal.h"
 #include "byhip_kernels.h"
@@ -292,6 +294,9 @@ __device__ __forceinline__ uint4 perm8(uint4 v) {
     return make_uint4(pair_lo(v.x, v.z), pair_hi(v.x, v.z), pair_lo(v.y, v.w), pair_hi(v.y, v.w));
 }
 
+// Floats between consecutive split-K partials (16-byte aligned).
+__host__ __device__ __forceinline__ size_t splitk_stride(int M, int N) { return ((size_t)M * N + 3) & ~(size_t)3; }
+
 template <int BM, int BN, int YT>
 __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
     using S = PipeShape<BM, BN>;
@@ -301,7 +306,10 @@ __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid / S::WGN, wn = wid % S::WGN;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-    const int K = a.K, nsteps = K / PBK;
+    const int K = a.K;
+    // K steps of this block: all of them, or split_steps from blockIdx.z * split_steps (split-K)
+    const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
+    const int nsteps = a.part ? min(a.split_steps, K / PBK - s_first) : K / PBK;
 
     // Rows past M / N read zeros through the buffer range checks (offsets stay below 2^32: the
     // launcher checks the sizes).
@@ -316,7 +324,7 @@ __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
     const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;  // group: 0 or 32 * 2^j
 
     auto gload = [&](PipeRegs& r, int s) {
-        const int k0 = min(s, nsteps - 1) * PBK;
+        const int k0 = (s_first + min(s, nsteps - 1)) * PBK;
         const v4u u0 = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 2u * k0, 0, 0);
         r.x0 = make_uint4(u0[0], u0[1], u0[2], u0[3]);
         if constexpr (S::XV == 16) {
@@ -415,6 +423,7 @@ __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
     if (s + 1 < nsteps) step(s + 1, r1, r2, s + 2 < nsteps);
     if (s + 2 < nsteps) step(s + 2, r2, r0, false);
 
+    float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -423,9 +432,232 @@ __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
-                if (m < a.M && n < a.N) store_y<YT>(a.y, (size_t)m * a.N + n, acc[i][j][r]);
+                if (m < a.M && n < a.N) {
+                    if (part) part[(size_t)m * a.N + n] = acc[i][j][r];
+                    else store_y<YT>(a.y, (size_t)m * a.N + n, acc[i][j][r]);
+                }
             }
         }
+}
+
+// y = sum over z of part[z] (z in order, so the result does not depend on block timing), four
+// consecutive outputs per thread.
+template <int YT>
+__global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part, int splits, int M, int N,
+                                                  void* y) {
+    const size_t mn = (size_t)M * N, stride = splitk_stride(M, N);
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    if (i + 4 <= mn) {
+        float4 t = *reinterpret_cast<const float4*>(part + i);
+        for (int z = 1; z < splits; ++z) {
+            const float4 v = *reinterpret_cast<const float4*>(part + (size_t)z * stride + i);
+            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+        }
+        store_y<YT>(y, i, t.x);
+        store_y<YT>(y, i + 1, t.y);
+        store_y<YT>(y, i + 2, t.z);
+        store_y<YT>(y, i + 3, t.w);
+    } else {
+        for (size_t e = i; e < mn; ++e) {
+            float t = part[e];
+            for (int z = 1; z < splits; ++z) t += part[(size_t)z * stride + e];
+            store_y<YT>(y, e, t);
+        }
+    }
+}
+
+// Skinny Q4 GEMM for small M (the decode-batch and short-prefill shapes): weights are read once,
+// straight from HBM into MFMA operand registers, so the kernel streams them like the GEMV while the
+// MFMAs do the row products. Same format conditions as q4_gemm_pipe, K % 128 == 0, M <= 32.
+//   Block: 4 waves on the same 64 columns (4 fragments of 16) and BM rows (BM / 16 fragments);
+//   the block's K steps of 128 are dealt round-robin to its waves, and the four partial tiles are
+//   added through LDS at the end (wave order 0 + 1 + 2 + 3).
+//   K order: in MFMA kk (0..3) of a step, lane group g (lanes 16g..16g+15) supplies the values
+//   32g + 8kk + (0, 4, 1, 5, 2, 6, 3, 7) of the step. A lane's weights for a step are then one
+//   16-byte load (one 32-value group, one scale); the (k, k+4) order is what the AND-OR
+//   dequantization yields, and perm8 gives the activations the same order. Both operands use it,
+//   so every product pairs the same k.
+//   Activations: each wave moves its step's BM x 128 slice straight from global memory into its
+//   own LDS buffer (16 lanes read a row's 256 bytes, so every load is a run of whole lines), with
+//   16-byte chunk c of row r at slot c ^ (r & 15): the fragment reads (16 rows, one chunk each)
+//   then hit 16 distinct bank groups. Each wave reads only what it loaded, so no barrier is
+//   needed; the double buffer and a vmcnt wait order the direct loads and the reads.
+template <int BM>
+struct SkinnyW {
+    v4u w[4];       // 32 nibbles of one column per fragment
+    uint32_t s[4];  // their fp16 scale
+};
+
+template <int BM>
+struct SkinnyLds {
+    static constexpr int kX = 4 * 2 * BM * 256;               // 4 waves x 2 buffers x BM rows x 256 bytes
+    static constexpr int kRed = 4 * (BM / 16) * 4 * 4 * 64 * 4;  // 4 partial tiles of BM x 64 floats
+    static constexpr int kBytes = kX > kRed ? kX : kRed;
+};
+
+template <int BM, int YT>
+__global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
+    constexpr int FM = BM / 16, FN = 4, NV = FM * FN * 4;  // accumulator floats per lane
+    constexpr int XDMA = BM / 4;                           // direct loads per step (4 rows each)
+    constexpr int XBUF = BM * 256;                         // bytes of one activation buffer
+    __shared__ __attribute__((aligned(16))) uint8_t lds[SkinnyLds<BM>::kBytes];
+
+    // wid is wave-uniform; readfirstlane tells the compiler so, which keeps the step logic in
+    // scalar registers and branches.
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 64, m0 = blockIdx.y * BM;
+    const int K = a.K;
+    const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
+    const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
+
+    // Rows past M and columns past N read zeros through the range checks (the launcher keeps the
+    // offsets below 2^31).
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
+    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
+    const rsrc_t sr = make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
+    const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
+    // Direct load u of a step: lane -> row 4u + lane / 16, LDS slot lane % 16 holding chunk
+    // slot ^ (row & 15) of that row.
+    uint32_t xo[XDMA];
+#pragma unroll
+    for (int u = 0; u < XDMA; ++u) {
+        const int r = 4 * u + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+        xo[u] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
+    }
+    uint32_t wo[FN], so[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        wo[j] = (uint32_t)(n0 + 16 * j + c) * (uint32_t)a.row_bytes + 16u * g;
+        so[j] = (uint32_t)(n0 + 16 * j + c) * (uint32_t)a.gpr;
+    }
+    uint8_t* const xbuf = lds + wid * 2 * XBUF;
+
+    // Step t of this wave is block step (wid + 4t + rot) mod nsteps. The rotation by the block
+    // index staggers where blocks start along K.
+    const int nt = nsteps > wid ? (nsteps - wid + 3) / 4 : 0;
+    const int rot = nsteps > 0 ? (int)(blockIdx.x % (unsigned)nsteps) : 0;
+    auto kstep = [&](int t) {
+        const int v = wid + 4 * t + rot;
+        return v >= nsteps ? v - nsteps : v;
+    };
+    // Every step issues the same loads: XDMA direct activation loads, then FN weight and FN scale
+    // loads. A step past the wave's last one (t >= nt) adds 2^31 through the scalar offset, which
+    // every resource rejects: it reads zeros without touching memory, so the loads need no branch
+    // around them and every step leaves the same number in flight.
+    auto load = [&](SkinnyW<BM>& r, uint8_t* __restrict__ dst, int t) {
+        const bool ok = t < nt;
+        const uint32_t k0 = (uint32_t)(s_first + (ok ? kstep(t) : 0)) * 128u;
+        const uint32_t oob = ok ? 0u : 0x80000000u;
+        const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
+#pragma unroll
+        for (int u = 0; u < XDMA; ++u)
+            lds_dma16(xr, dst + 1024 * u, xo[u] + 2u * k0, oob);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo[j] + (k0 >> 1), oob, 2);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (so[j] + grp), oob, 0);
+    };
+
+    const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
+    const h2 zz_lo = {zlo, zlo}, zz_hi = {zhi, zhi};
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
+
+    f4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const SkinnyW<BM>& r, const uint8_t* __restrict__ src) {
+        h2 ss[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const _Float16 sc = bits_h((uint16_t)r.s[j]);
+            ss[j] = (h2){sc, sc};
+        }
+        uint4 xv[4][FM];  // the step's activation fragments, all read before the math
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                xv[kk][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            h8 bw[FN], ax[FM];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint4 u = perm8(xv[kk][i]);
+                ax[i] = *reinterpret_cast<const h8*>(&u);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint32_t d = r.w[j][kk], d8 = d >> 8;
+                const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
+                const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
+                const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
+                const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
+                const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss[j]), h2_bits((q1 - zz_hi) * ss[j]),
+                                           h2_bits((q2 - zz_lo) * ss[j]), h2_bits((q3 - zz_hi) * ss[j]));
+                bw[j] = *reinterpret_cast<const h8*>(&u);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Two register sets and two LDS buffers: the loads of the wave's next step are in flight while
+    // this one computes. The scheduling barriers keep each step's loads ahead of its math in issue
+    // order; the wait leaves exactly the next step's loads in flight, so this step's activations
+    // have landed in LDS (the compiler cannot see that dependence) and its weights and scales are
+    // in registers.
+    SkinnyW<BM> ra, rb;
+    load(ra, xbuf, 0);
+    auto step = [&](int t, const SkinnyW<BM>& cur, SkinnyW<BM>& nxt, const uint8_t* __restrict__ xcur,
+                    uint8_t* __restrict__ xnxt) {
+        __builtin_amdgcn_sched_barrier(0);
+        load(nxt, xnxt, t + 1);
+        wait_vmcnt<XDMA + 2 * FN>();
+        __builtin_amdgcn_sched_barrier(0);
+        compute(cur, xcur);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int t = 0; t < nt; t += 2) {
+        step(t, ra, rb, xbuf, xbuf + XBUF);
+        if (t + 1 >= nt) break;
+        step(t + 1, rb, ra, xbuf + XBUF, xbuf);
+    }
+
+    // Partial tiles of the four waves -> LDS (over the activation buffers, once every wave is done
+    // with them and every direct load has landed) -> sum in wave order -> y or the split-K partials.
+    wait_vmcnt<0>();
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);  // [4][NV][64]
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(wid * NV + (i * FN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    __syncthreads();
+    float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
+    for (int e = threadIdx.x; e < NV * 64; e += 256) {
+        const int v = e >> 6, l = e & 63;
+        const float sum = red[(0 * NV + v) * 64 + l] + red[(1 * NV + v) * 64 + l] +
+                          red[(2 * NV + v) * 64 + l] + red[(3 * NV + v) * 64 + l];
+        const int i = v / (FN * 4), j = (v >> 2) % FN, r = v & 3;
+        const int m = m0 + 16 * i + 4 * (l >> 4) + r, n = n0 + 16 * j + (l & 15);
+        if (m < a.M && n < a.N) {
+            if (part) part[(size_t)m * a.N + n] = sum;
+            else store_y<YT>(a.y, (size_t)m * a.N + n, sum);
+        }
+    }
 }
 
 // Whether the pipelined Q4 kernel takes these arguments.
@@ -438,9 +670,20 @@ bool q4_pipe_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 128) * a.gpr * 2 < kOutOfRange;
 }
 
+template <int BM>
+void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
+    const dim3 grid((a.N + 63) / 64, (a.M + BM - 1) / BM, splits);
+    switch (a.y_dtype) {
+    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
+    default: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_BF16>), grid, dim3(256), 0, stream(), a); break;
+    }
+    BYHIP_LAUNCHED("q4_gemm_skinny");
+}
+
 template <int BM, int BN>
-void launch_q4_pipe_shape(const GemmArgs& a) {
-    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+void launch_q4_pipe_shape(const GemmArgs& a, int splits) {
+    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
     case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
     case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
@@ -449,23 +692,69 @@ void launch_q4_pipe_shape(const GemmArgs& a) {
     BYHIP_LAUNCHED("q4_gemm_pipe");
 }
 
-// Tile choice: 64 x 128 when that gives at least one block per CU, else 64 x 64; 32-row tiles when
-// M <= 32 (32 x 128 if that fills the chip, else 32 x 64). BYHIP_Q4_TILE=1..4 forces 64x128,
-// 64x64, 32x128, 32x64.
-void launch_q4_pipe(const GemmArgs& a) {
+// Split-K for a grid of `tiles` blocks over `nsteps` K steps: when the tiles leave CUs idle, K is
+// split so that the grid holds about two blocks per CU, each split keeping at least `min_steps`
+// steps; the partials must fit the workspace. BYHIP_Q4_SPLIT forces the number of splits. Sets
+// a.part / a.split_steps and returns the number of splits (1: none).
+int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps) {
     const long cus = compute_units();
-    auto blocks = [&](int bm, int bn) { return (long)((a.N + bn - 1) / bn) * ((a.M + bm - 1) / bm); };
+    long splits = env_int("BYHIP_Q4_SPLIT", 0);
+    if (splits < 1) splits = tiles >= cus ? 1 : std::min<long>((2 * cus + tiles - 1) / tiles, nsteps / min_steps);
+    const long fit = (long)(kWorkspaceBytes / (splitk_stride(a.M, a.N) * sizeof(float)));
+    splits = std::max<long>(1, std::min<long>({splits, (long)nsteps, fit}));
+    if (splits == 1) return 1;
+    a.split_steps = (int)((nsteps + splits - 1) / splits);
+    a.part = static_cast<float*>(workspace());
+    return (nsteps + a.split_steps - 1) / a.split_steps;  // no empty split
+}
+
+void launch_splitk_sum(const GemmArgs& a, int splits) {
+    const size_t quads = ((size_t)a.M * a.N + 3) / 4;
+    const dim3 grid((unsigned)((quads + 255) / 256));
+    switch (a.y_dtype) {
+    case BYHIP_F32: hipLaunchKernelGGL(splitk_sum<BYHIP_F32>, grid, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
+    case BYHIP_F16: hipLaunchKernelGGL(splitk_sum<BYHIP_F16>, grid, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
+    default: hipLaunchKernelGGL(splitk_sum<BYHIP_BF16>, grid, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
+    }
+    BYHIP_LAUNCHED("splitk_sum");
+}
+
+// Tile choice: 64 x 128, or 32 x 128 when M <= 32, split along K when the tiles leave CUs idle.
+// BYHIP_Q4_TILE=1..4 forces 64x128, 64x64, 32x128, 32x64.
+void launch_q4_pipe(const GemmArgs& a0) {
+    GemmArgs a = a0;
     int tile = env_int("BYHIP_Q4_TILE", 0);
-    if (tile < 1 || tile > 4) {
-        if (a.M <= 32) tile = blocks(32, 128) >= cus ? 3 : 4;
-        else tile = blocks(64, 128) >= cus ? 1 : 2;
-    }
+    if (tile < 1 || tile > 4) tile = a.M <= 32 ? 3 : 1;
+    const int bm = tile <= 2 ? 64 : 32, bn = tile % 2 ? 128 : 64;
+    const long tiles = (long)((a.N + bn - 1) / bn) * ((a.M + bm - 1) / bm);
+    const int splits = choose_split(a, tiles, a.K / PBK, 4);
     switch (tile) {
-    case 1: launch_q4_pipe_shape<64, 128>(a); break;
-    case 2: launch_q4_pipe_shape<64, 64>(a); break;
-    case 3: launch_q4_pipe_shape<32, 128>(a); break;
-    default: launch_q4_pipe_shape<32, 64>(a); break;
+    case 1: launch_q4_pipe_shape<64, 128>(a, splits); break;
+    case 2: launch_q4_pipe_shape<64, 64>(a, splits); break;
+    case 3: launch_q4_pipe_shape<32, 128>(a, splits); break;
+    default: launch_q4_pipe_shape<32, 64>(a, splits); break;
     }
+    if (a.part) launch_splitk_sum(a, splits);
+}
+
+// Whether the skinny kernel takes the call: the pipelined kernel's conditions, K % 128 == 0, all
+// operand offsets below 2^31, and M up to 32 (BYHIP_Q4_SKINNY_MAX_M lowers the limit).
+bool q4_skinny_ok(const GemmArgs& a) {
+    constexpr uint64_t kLim = 0x80000000u;  // offsets stay below 2^31 (the kernel's out-of-range steps)
+    return a.K % 128 == 0 && a.M <= std::min(32, env_int("BYHIP_Q4_SKINNY_MAX_M", 32)) && q4_pipe_ok(a) &&
+           (uint64_t)(a.M + 64) * a.K * 2 < kLim && (uint64_t)(a.N + 64) * a.row_bytes < kLim &&
+           (uint64_t)(a.N + 64) * a.gpr * 2 < kLim;
+}
+
+// Rows per block: 16 or 32 (the smallest that holds M).
+void launch_q4_skinny(const GemmArgs& a0) {
+    GemmArgs a = a0;
+    const int bm = a.M <= 16 ? 16 : 32;
+    const long tiles = (a.N + 63) / 64;
+    const int splits = choose_split(a, tiles, a.K / 128, 8);
+    if (bm == 16) launch_q4_skinny_shape<16>(a, splits);
+    else launch_q4_skinny_shape<32>(a, splits);
+    if (a.part) launch_splitk_sum(a, splits);
 }
 
 template <BFormat F, bool XF32>
@@ -499,7 +788,8 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.M > 65535 * BM) fail("byhip: M=%d too large for one launch", a.M);
     switch (fmt) {
     case BFormat::Q4Fast:
-        if (q4_pipe_ok(a)) launch_q4_pipe(a);
+        if (q4_skinny_ok(a)) launch_q4_skinny(a);
+        else if (q4_pipe_ok(a)) launch_q4_pipe(a);
         else launch_f<BFormat::Q4Fast>(a);
         break;
     case BFormat::Q4Generic: launch_f<BFormat::Q4Generic>(a); break;

@@ -41,6 +41,11 @@ void enter_compute();
 void no_host_sync(const char* what);
 hipStream_t stream();
 int compute_units();
+// Device scratch for kernels that need it (split-K partial sums), allocated once at init so that
+// no GEMM call allocates (calls may be captured into a recording). Work queued on the library
+// stream uses it in stream order.
+constexpr size_t kWorkspaceBytes = 32u << 20;
+void* workspace();
 
 // Allocation registry of buffers the library handed out: byte size (0 = not ours) and, for small
 // host uploads, a host copy (decode tables are classified on the host without a device read).

@@ -106,4 +106,21 @@ __device__ __forceinline__ void store_y(void* y, size_t idx, float v) {
     }
 }
 
+// LDS pointer type of the direct global-to-LDS loads (buffer_load ... lds).
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane from a buffer straight into LDS: lane l writes dst + 16 l. Completion counts in
+// vmcnt like any buffer load.
+__device__ __forceinline__ void lds_dma16(rsrc_t r, void* dst, uint32_t voffset, uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, voffset, soffset, 0, 0);
+}
+
+// s_waitcnt with vmcnt = N and lgkmcnt / expcnt left open (gfx9 encoding: vmcnt[3:0] and
+// vmcnt[5:4] at bits 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace byhip

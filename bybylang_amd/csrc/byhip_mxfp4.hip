@@ -66,8 +66,6 @@ constexpr int kScaleDma = 2;                                 // per lane per 4-s
 constexpr int kOutPitch = 128 + 4;                           // floats per staged output row
 constexpr int kOutWaveBytes = 32 * kOutPitch * 4;            // 32 rows per wave and pass
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 2)) & 3; }
 
 __device__ __forceinline__ i8v operand(uint4 u) {
@@ -87,14 +85,6 @@ template <int PI, int PJ>
 __device__ __forceinline__ f4 mx_mfma(uint4 a, uint4 b, f4 acc, int sa, int sb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(operand(a), operand(b), acc, 4, 4, 2 * PI, sa,
                                                               2 * PJ, sb);
-}
-
-// s_waitcnt with vmcnt = N and lgkmcnt / expcnt left open (gfx9 encoding: vmcnt[3:0] and
-// vmcnt[5:4] at bits 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // Workgroup barrier after this wave's LDS reads and all but the newest N direct loads have

@@ -29,6 +29,7 @@ struct State {
     hipStream_t stream = nullptr;
     hipDeviceProp_t prop{};
     std::unordered_map<const void*, Alloc> allocs;
+    void* workspace = nullptr;  // kWorkspaceBytes, allocated by byhip_init, kept until exit
     // session
     bool session_open = false;
     std::vector<void*> deferred_frees;
@@ -90,6 +91,7 @@ void enter_compute() {
 
 hipStream_t stream() { return st().stream; }
 int compute_units() { return st().prop.multiProcessorCount; }
+void* workspace() { return st().workspace; }
 
 void no_host_sync(const char* what) {
     if (st().recording)
@@ -194,6 +196,7 @@ int byhip_init(int device) {
         BYHIP_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
         BYHIP_HIP(hipEventCreate(&s.ev_begin));
         BYHIP_HIP(hipEventCreate(&s.ev_end));
+        BYHIP_HIP(hipMalloc(&s.workspace, kWorkspaceBytes));
         s.device = device;
         s.inited = true;
     });

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from oracle_lib import OP_Q4_COOP_GEMM, OP_Q4_GEMV, q4_blob, shape_op_program
-from parity import TIER_F32_ACC, bf16_bits_to_f32, f32_to_bf16_rne, ref_check, tier_check
+from parity import TIER_BF16_OUT, TIER_F32_ACC, bf16_bits_to_f32, f32_to_bf16_rne, ref_check, tier_check
 
 pytestmark = pytest.mark.gpu
 
@@ -122,7 +122,7 @@ def test_q4_dtypes_and_rows(hip, oracle, M, x_dtype, y_dtype):
         want_r = want.astype(np.float16).astype(np.float32)
         tier_check(got, want_r, TIER_F32_ACC)
     elif y_dtype == "bf16":
-        tier_check(got, f32_to_bf16_rne(want).reshape(M, N), 4e-3)
+        tier_check(got, f32_to_bf16_rne(want).reshape(M, N), TIER_BF16_OUT)
     elif M <= 8:
         ref_check(got, want)
     else:
@@ -132,12 +132,13 @@ def test_q4_dtypes_and_rows(hip, oracle, M, x_dtype, y_dtype):
 @pytest.mark.parametrize("tile", [1, 2, 3, 4])
 @pytest.mark.parametrize("shape", [(64, 512, 256), (130, 256, 200), (24, 640, 136), (33, 128, 64)])
 def test_q4_gemm_tiles(hip, oracle, monkeypatch, tile, shape):
-    """Every tile shape of the pipelined Q4 GEMM (64x128, 64x64, 32x128, 32x64, forced through
-    BYHIP_Q4_TILE), on ragged M and N and short K, fp16 in and out, against the oracle."""
+    """Every tile shape of the pipelined (LDS-staged) Q4 GEMM (64x128, 64x64, 32x128, 32x64, forced
+    through BYHIP_Q4_TILE), on ragged M and N and short K, fp16 in and out, against the oracle."""
     from bybylang_amd import synth
     M, K, N = shape
     monkeypatch.setenv("BYHIP_Q4_TILE", str(tile))
     monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_SKINNY_MAX_M", "0")  # the LDS-staged kernel for every M
     g = synth.rng(7000 + 17 * M + N)
     wq, sc, ze, _ = synth.q4_weights(g, N, K)
     x = synth.activations(g, M, K, np.float16)
@@ -145,6 +146,75 @@ def test_q4_gemm_tiles(hip, oracle, monkeypatch, tile, shape):
     got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, hip.F16)
     want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
     tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5])
+@pytest.mark.parametrize("shape", [(64, 512, 256), (33, 640, 136), (130, 1024, 200)])
+@pytest.mark.parametrize("y_dtype", ["F32", "F16", "BF16"])
+def test_q4_gemm_split_k(hip, oracle, monkeypatch, splits, shape, y_dtype):
+    """Split-K (forced through BYHIP_Q4_SPLIT): partial sums over K slices added in slice order
+    by a second kernel, every output dtype, ragged shapes, against the oracle; a repeat call is
+    bit-identical (the sum order does not depend on block timing)."""
+    from bybylang_amd import synth
+    M, K, N = shape
+    monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_SKINNY_MAX_M", "0")  # the LDS-staged kernel for every M
+    g = synth.rng(7100 + 13 * M + N + splits)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    yt = getattr(hip, y_dtype)
+    print(f"q4 split-k splits={splits} M={M} K={K} N={N} y={y_dtype}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, yt)
+    again, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, yt)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    if y_dtype == "F16":
+        want = want.astype(np.float16).astype(np.float32)
+    elif y_dtype == "BF16":
+        want = f32_to_bf16_rne(want)
+    tier_check(got, want.reshape(M, N), TIER_F32_ACC if y_dtype != "BF16" else TIER_BF16_OUT)
+
+
+@pytest.mark.parametrize("M", [9, 16, 17, 32, 40, 64])
+@pytest.mark.parametrize("splits", [0, 3])
+@pytest.mark.parametrize("group", [32, 128, 0])
+def test_q4_gemm_skinny(hip, oracle, monkeypatch, M, splits, group):
+    """The skinny small-M kernel (weights straight to MFMA registers, K split over the block's
+    waves): 16-, 32- and 64-row blocks, ragged M and N, groups 32 / 128 / whole row, with and
+    without split-K, fp16 in and out, against the oracle."""
+    from bybylang_amd import synth
+    K, N = 768, 200
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    if splits:
+        monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
+    g = synth.rng(7300 + 7 * M + group + splits)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K, group if group else K)
+    gpr = K // group if group else 1
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 skinny M={M} splits={splits} group={group}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, group, gpr)
+    tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("M", [32, 256])
+def test_q4_layer_down_auto_split(hip, oracle, M):
+    """The layer batch's down projection (K=14336, N=4096) at M=32 and 256, where the tiles alone
+    leave most CUs idle and the launcher splits K; rows against the oracle, every row against an
+    fp64 product of the fp16-rounded weights."""
+    from bybylang_amd import synth
+    g = synth.rng(40 + M)
+    K, N = 14336, 4096
+    wq, sc, ze, codes = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 down auto split M={M}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, hip.F16)
+    xf = x.astype(np.float32).reshape(-1)
+    want = oracle.matmul_q4(xf, wq, sc, ze, M, K, N, 32, K // 32, rows=(M - 4, M))[M - 4:M]
+    tier_check(got[M - 4:M], want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+    w = (codes.astype(np.float32) * np.repeat(sc.reshape(N, -1), 32, axis=1)).astype(np.float64)
+    tier_check(got, x.astype(np.float64) @ w.T, TIER_F32_ACC)
 
 
 @pytest.mark.parametrize("case", ["group0", "group64", "group128", "asym_zero", "int_zero5",
