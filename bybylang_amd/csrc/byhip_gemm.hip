@@ -449,10 +449,19 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
     const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
     if (i + 4 <= mn) {
-        float4 t = *reinterpret_cast<const float4*>(part + i);
-        for (int z = 1; z < splits; ++z) {
-            const float4 v = *reinterpret_cast<const float4*>(part + (size_t)z * stride + i);
-            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+        // The slices are loaded eight at a time before they are added, so their latencies overlap.
+        float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int z0 = 0; z0 < splits; z0 += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (z0 + u < splits) v[u] = *reinterpret_cast<const float4*>(part + (size_t)(z0 + u) * stride + i);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (z0 + u < splits) {
+                    if (z0 + u == 0) t = v[0];
+                    else { t.x += v[u].x; t.y += v[u].y; t.z += v[u].z; t.w += v[u].w; }
+                }
         }
         store_y<YT>(y, i, t.x);
         store_y<YT>(y, i + 1, t.y);
@@ -470,7 +479,8 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 // Skinny Q4 GEMM for small M (the decode-batch and short-prefill shapes): weights are read once,
 // straight from HBM into MFMA operand registers, so the kernel streams them like the GEMV while the
 // MFMAs do the row products. Same format conditions as q4_gemm_pipe, K % 128 == 0, M <= 32.
-//   Block: 4 waves on the same 64 columns (4 fragments of 16) and BM rows (BM / 16 fragments);
+//   Block: 4 waves on the same kSkinnyCols columns (fragments of 16) and BM rows (BM / 16
+//   fragments);
 //   the block's K steps of 128 are dealt round-robin to its waves, and the four partial tiles are
 //   added through LDS at the end (wave order 0 + 1 + 2 + 3).
 //   K order: in MFMA kk (0..3) of a step, lane group g (lanes 16g..16g+15) supplies the values
@@ -483,22 +493,25 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 //   16-byte chunk c of row r at slot c ^ (r & 15): the fragment reads (16 rows, one chunk each)
 //   then hit 16 distinct bank groups. Each wave reads only what it loaded, so no barrier is
 //   needed; the double buffer and a vmcnt wait order the direct loads and the reads.
+constexpr int kSkinnyFN = 4;                 // column fragments per block (and per wave)
+constexpr int kSkinnyCols = 16 * kSkinnyFN;  // columns per block
+
 template <int BM>
 struct SkinnyW {
-    v4u w[4];       // 32 nibbles of one column per fragment
-    uint32_t s[4];  // their fp16 scale
+    v4u w[kSkinnyFN];       // 32 nibbles of one column per fragment
+    uint32_t s[kSkinnyFN];  // their fp16 scale
 };
 
 template <int BM>
 struct SkinnyLds {
     static constexpr int kX = 4 * 2 * BM * 256;               // 4 waves x 2 buffers x BM rows x 256 bytes
-    static constexpr int kRed = 4 * (BM / 16) * 4 * 4 * 64 * 4;  // 4 partial tiles of BM x 64 floats
+    static constexpr int kRed = 4 * (BM / 16) * kSkinnyFN * 4 * 64 * 4;  // 4 partial tiles of the block
     static constexpr int kBytes = kX > kRed ? kX : kRed;
 };
 
 template <int BM, int YT>
 __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
-    constexpr int FM = BM / 16, FN = 4, NV = FM * FN * 4;  // accumulator floats per lane
+    constexpr int FM = BM / 16, FN = kSkinnyFN, NV = FM * FN * 4;  // accumulator floats per lane
     constexpr int XDMA = BM / 4;                           // direct loads per step (4 rows each)
     constexpr int XBUF = BM * 256;                         // bytes of one activation buffer
     __shared__ __attribute__((aligned(16))) uint8_t lds[SkinnyLds<BM>::kBytes];
@@ -507,7 +520,7 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     // scalar registers and branches.
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 64, m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * kSkinnyCols, m0 = blockIdx.y * BM;
     const int K = a.K;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
     const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
@@ -672,7 +685,7 @@ bool q4_pipe_ok(const GemmArgs& a) {
 
 template <int BM>
 void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
-    const dim3 grid((a.N + 63) / 64, (a.M + BM - 1) / BM, splits);
+    const dim3 grid((a.N + kSkinnyCols - 1) / kSkinnyCols, (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
     case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
     case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
@@ -750,7 +763,7 @@ bool q4_skinny_ok(const GemmArgs& a) {
 void launch_q4_skinny(const GemmArgs& a0) {
     GemmArgs a = a0;
     const int bm = a.M <= 16 ? 16 : 32;
-    const long tiles = (a.N + 63) / 64;
+    const long tiles = (a.N + kSkinnyCols - 1) / kSkinnyCols;
     const int splits = choose_split(a, tiles, a.K / 128, 8);
     if (bm == 16) launch_q4_skinny_shape<16>(a, splits);
     else launch_q4_skinny_shape<32>(a, splits);

@@ -3,11 +3,13 @@
 // y[m, n] = sum_k x[m, k] * ((float)q[n, k] - zero[n, g]) * scale[n, g] with fp32 accumulation
 // (cpu_kernels_impl.inc:293-319, cpu_vm.c:420-482).
 //
-// Work split: a wave owns R consecutive weight rows (8 when a row is at most two 32-value chunks per
-// lane); lane l holds chunks l, l + 64, ... of every row, each chunk one 16-byte load of 32 nibbles.
+// Work split: a wave owns R consecutive weight rows (4 or 8 when a row is at most two 32-value chunks
+// per lane); lane l holds chunks l, l + 64, ... of every row, each chunk one 16-byte load of 32
+// nibbles.
 // Per wave the loads go out in this order, all before the first wait: the block's activations, the
-// scales (one 16-byte load per chunk covers 8 rows in the resident layout), then the weight rows;
-// the wait counter completes in issue order, so row r is processed as soon as it lands.
+// scales (one load per chunk covers the wave's rows: the resident layout blocks them by 8), then the
+// weight rows; the wait counter completes in issue order, so row r is processed as soon as it
+// lands.
 //
 // Activations are staged once per 256-thread block in LDS: each 32-value chunk as 16 fp16 pairs
 // (x[8j+i], x[8j+i+4]) matching the nibble pairs below, with its sums of x.
@@ -33,8 +35,10 @@ typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 // Weight rows a wave keeps in flight: 8 rows of up to two chunks per lane, fewer when each row
-// needs more chunks (16 chunk loads in flight per lane at most).
-constexpr int gemv_rows(int cpl) { return cpl >= 8 ? 2 : (cpl >= 4 ? 4 : 8); }
+// needs more chunks (16 chunk loads in flight per lane at most). A single activation row takes 4:
+// twice the waves, so the dequantization and reduction left after the last loads land are spread
+// thinner (measured faster on the decode shapes; with several rows the larger batch wins).
+constexpr int gemv_rows(int m, int cpl) { return cpl >= 8 ? 2 : (cpl >= 4 || m == 1 ? 4 : 8); }
 
 struct GemvArgs {
     const void* x;
@@ -68,7 +72,7 @@ __device__ __forceinline__ void load_bytes(rsrc_t r, uint32_t off, uint32_t* w) 
 template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK, int YT>
 __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     constexpr int XS = XF32 ? 2 : 1;
-    constexpr int R = gemv_rows(CPL);
+    constexpr int R = gemv_rows(M, CPL);
     constexpr uint32_t XB = XF32 ? 4 : 2;  // bytes per activation
     constexpr int XW = XF32 ? 8 : 4;       // 16-byte activation loads per 32-value chunk
     constexpr int XC = 2;                  // activation chunks a thread stages (M * G <= 512)
@@ -314,7 +318,7 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
 
 template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK>
 void launch_y(const GemvArgs& a, int y_dtype) {
-    constexpr int R = gemv_rows(CPL);
+    constexpr int R = gemv_rows(M, CPL);
     const int G = a.K / 32;
     const size_t lds = (size_t)M * G * 16 * 4 * (XF32 ? 2 : 1) + (size_t)M * G * 2 * 4;
     const int grid = (a.N + 4 * R - 1) / (4 * R);  // one batch of rows per wave
