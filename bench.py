@@ -185,6 +185,67 @@ def bench_c4(dev, synth, steps, warmup):
         for w in ws:
             w.close()
     out["weight_copies"] = copies
+    out["M1_fused"] = bench_c4_fused(dev, synth, steps, warmup)
+    return out
+
+
+# The same decode layer (M = 1) through the fused entry point (sessionMatmulQ4Fused): attention
+# norm + QKV as three matrices sharing the input, O + residual, MLP norm + silu(gate) * up, down +
+# residual. fp32 input, outputs, norm weights and residual, as the reference's session ops.
+C4_FUSED = [("qkv_norm", 0, 4096, [4096, 1024, 1024], True, False),
+            ("o_res", 0, 4096, [4096], False, True),
+            ("gate_up_norm_silu", 1, 4096, [14336, 14336], True, False),
+            ("down_res", 0, 14336, [4096], False, True)]
+
+
+def fused_bytes(mode, K, Ns, norm, res):
+    """Weights (nibbles, fp16 scales) plus fp32 input, outputs (one in mode 1), norm weights and
+    residual."""
+    w = sum(N * K // 2 + N * (K // 32) * 2 for N in Ns)
+    n_out = Ns[0] if mode == 1 else sum(Ns)
+    return w + K * 4 + n_out * 4 + (K * 4 if norm else 0) + (max(Ns) * 4 if res else 0)
+
+
+def bench_c4_fused(dev, synth, steps, warmup):
+    layer_bytes = sum(fused_bytes(md, K, Ns, nm, rs) for _, md, K, Ns, nm, rs in C4_FUSED)
+    copies = max(1, -(-ROTATE_BYTES // layer_bytes))
+    g = synth.rng(44)
+    ops = []
+    for name, mode, K, Ns, norm, res in C4_FUSED:
+        mats = []
+        for N in Ns:
+            wq, sc, ze, _ = synth.q4_weights(g, N, K)
+            mats.append([dev.Q4Weights(wq, sc, ze, K, N, 32, K // 32) for _ in range(copies)])
+        a = dev.DeviceBuffer.from_array(g.standard_normal(K).astype(np.float32))
+        outs = [dev.DeviceBuffer(N * 4) for N in Ns]
+        gamma = dev.DeviceBuffer.from_array((1.0 + 0.1 * g.standard_normal(K)).astype(np.float32)) if norm else None
+        r = dev.DeviceBuffer.from_array(g.standard_normal(max(Ns)).astype(np.float32)) if res else None
+        ops.append((name, mode, K, Ns, norm, res, mats, a, outs, gamma, r))
+
+    def call(op, i):
+        name, mode, K, Ns, norm, res, mats, a, outs, gamma, r = op
+        rc = dev.q4_matmul_fused(mode, a, [m[i % copies] for m in mats], outs, r, gamma, 1e-5)
+        assert rc == 0, f"fused {name} unsupported"
+
+    out = {"per_op": {}}
+    for op in ops:
+        name, mode, K, Ns, norm, res = op[:6]
+        gpu_s, _ = run_steps(lambda i, op=op: call(op, i), steps, warmup)
+        per = gpu_s / steps
+        out["per_op"][name] = {"us": per * 1e6, "GBps": fused_bytes(mode, K, Ns, norm, res) / per / 1e9}
+
+    def layer(i):
+        for op in ops:
+            call(op, i)
+
+    gpu_s, _ = run_steps(layer, steps, warmup)
+    per = gpu_s / steps
+    out.update({"batch_us": per * 1e6, "batch_GBps": layer_bytes / per / 1e9, "weight_copies": copies,
+                "launches": len(C4_FUSED)})
+    for op in ops:
+        for m in op[6]:
+            for w in m:
+                w.close()
     return out
 
 

@@ -11,4 +11,12 @@ bool q4_gemv_eligible(const byhip_q4w* w, int M, int x_dtype);
 // Queues y[M, N] = x[M, K] . W^T (M <= 8 runs as launches of up to 4 activation rows).
 void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
 
+// The fused decode GEMV of sessionMatmulQ4Fused: BYHIP_OK when the kernel takes these weights for
+// this mode (1..3 weights for mode 0, gate and up of equal N for mode 1, equal K / group / groups
+// per row and scale formats, the decode layout present), else BYHIP_UNSUPPORTED.
+int q4_fused_check(int mode, const byhip_q4w* const* ws, int n_ws);
+// Queues it (fp32 input, outputs, residual and norm weights; res / gamma null when absent).
+void launch_q4_gemv_fused(int mode, const float* x, const byhip_q4w* const* ws, int n_ws, float* const* outs,
+                          const float* res, const float* gamma, float eps);
+
 }  // namespace byhip

@@ -375,6 +375,283 @@ int gemv_cpl(int K) {
     return cpl;
 }
 
+// ---- fused decode GEMV (sessionMatmulQ4Fused, gpubackend.nim:3185-3231) ----------------------
+//
+// M = 1, fp32 input and outputs, resident weights with the blocked scale copy. The shader it
+// replaces (q4_autotune.nim:194-330) computes, per output row, sum_k ((q - z) * s) * x[k] with
+// x[k] = a[k] * gamma[k] under RMSNorm, scales the sum by inv = 1 / sqrt(sum a^2 / K + eps), and
+// in mode 1 returns silu(gate) * up; the residual is added last.
+//   mode 0: up to three matrices share the input; a wave's batch of 4 rows lies in one matrix
+//   (batches are numbered per matrix), so the matrix is wave-uniform.
+//   mode 1: a wave loads 4 rows of gate and the same 4 rows of up.
+// The input is staged once per block as in q4_gemv (fp16 hi/lo pairs in the (k, k+4) order of the
+// nibble pairs, and the chunk sums for the zero point), after the norm weight is applied; the
+// block also sums a^2 for the norm factor (partials per thread, added in a fixed order).
+struct FusedMat {
+    const uint8_t* wq;
+    const void* sblk;   // [ceil(N/8)][K/32][8] scales (fp16 or fp32)
+    const float* zblk;  // same layout, fp32 zeros; null when the zero point is uniform
+    float zero_value;
+    float* y;
+    int N, n_pad, batch0;  // batch0: the first row batch of this matrix in the wave numbering
+};
+
+struct FusedArgs {
+    const float* x;
+    const float* res;    // null: no residual
+    const float* gamma;  // null: no RMSNorm
+    float eps;
+    int K, row_bytes, nmats, batches;
+    FusedMat m[3];
+};
+
+// Rows per wave and matrix: 4, or 2 when a row takes 8 chunks per lane (the weights a wave keeps
+// in flight).
+constexpr int fused_rows(int cpl) { return cpl >= 8 ? 2 : 4; }
+
+template <int CPL, bool SF16, bool ZU, int MODE>
+__global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
+    constexpr int R = fused_rows(CPL);
+    constexpr int NM = MODE == 1 ? 2 : 1;  // matrices a wave reads
+    constexpr uint32_t SB = SF16 ? 2u : 4u;
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int K = a.K, G = K >> 5;
+    uint32_t* xh = lds;                                      // [G][16] fp16 pairs, high terms
+    uint32_t* xl = xh + G * 16;                              // [G][16] low terms
+    float* sums = reinterpret_cast<float*>(xl + G * 16);     // [G] sum of x over the chunk
+    float* ssq_part = sums + G;                              // [256]
+
+    const int wb = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (tid >> 6));
+    const bool live = wb < a.batches;  // uniform in the wave; every wave takes part in the barrier
+    int mi = 0;
+    if (MODE == 0) {
+        if (a.nmats > 1 && wb >= a.m[1].batch0) mi = 1;
+        if (a.nmats > 2 && wb >= a.m[2].batch0) mi = 2;
+    }
+    const FusedMat& fm0 = a.m[mi];
+    const int n0 = (wb - fm0.batch0) * R;  // first matrix-local row of the wave
+
+    // This lane's chunks (chunks past K are clamped onto the last one and their scale is zeroed).
+    uint32_t coff[CPL];
+    bool cv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int ci = lane + kWave * c;
+        cv[c] = ci < G;
+        coff[c] = (uint32_t)min(ci, G - 1) * 16u;
+    }
+
+    // 1. the first input chunk this thread stages (chunk tid; chunk tid + 256 follows after the
+    // weight loads are out) and its norm weights
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)K * 4u);
+    const rsrc_t gr = make_rsrc(a.gamma ? a.gamma : a.x, a.gamma ? (uint32_t)K * 4u : 0u);
+    auto load_chunk = [&](int idx, uint4* xraw, uint4* graw) {
+        const uint32_t base = idx < G ? (uint32_t)idx * 128u : kOutOfRange;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xraw[t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
+        if (a.gamma) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) graw[t] = buf_load16(gr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
+        }
+    };
+    uint4 xraw[8], graw[8];
+    load_chunk(tid, xraw, graw);
+
+    // 2. scales and zeros, 3. weight rows of the wave's batch (per matrix), all before the first wait
+    uint32_t sraw[NM][R][CPL], zraw[NM][R][CPL];
+    uint4 wv[NM][R][CPL];
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+        const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
+        const rsrc_t sr = make_rsrc(fm.sblk, (uint32_t)fm.n_pad * (uint32_t)G * SB);
+        const rsrc_t zr = make_rsrc(ZU ? fm.sblk : fm.zblk, ZU ? 0u : (uint32_t)fm.n_pad * (uint32_t)G * 4u);
+        const int nb = min(n0, fm.n_pad - R);  // R divides 8 and n0, so the rows sit in one block of 8
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t e = ((uint32_t)(nb >> 3) * (uint32_t)G + (coff[c] >> 4)) * 8u + (uint32_t)(nb & 7);
+            uint32_t sw[R * SB / 4];
+            load_bytes<R * SB>(sr, e * SB, sw);
+#pragma unroll
+            for (int r = 0; r < R; ++r) sraw[j][r][c] = SF16 ? ((sw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu) : sw[r];
+            if constexpr (!ZU) {
+                uint32_t zw[R];
+                load_bytes<R * 4>(zr, e * 4u, zw);
+#pragma unroll
+                for (int r = 0; r < R; ++r) zraw[j][r][c] = zw[r];
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+        const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
+        const rsrc_t wr = make_rsrc(fm.wq, (uint32_t)fm.N * (uint32_t)a.row_bytes);
+        // chunk-major, the order step 5 consumes them in
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t roff = (uint32_t)min(n0 + r, fm.N - 1) * (uint32_t)a.row_bytes;
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wr, coff[c], roff, 2);
+                wv[j][r][c] = make_uint4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load is out before the first wait
+
+    // 4. stage the input: x = a * gamma under the norm, fp16 hi/lo pairs, chunk sums, sum of a^2
+    float ssq = 0.0f;
+    auto stage_chunk = [&](int idx, const uint4* xraw, const uint4* graw) {
+        if (idx >= G) return;
+        float v[32];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            v[4 * t] = __builtin_bit_cast(float, xraw[t].x);
+            v[4 * t + 1] = __builtin_bit_cast(float, xraw[t].y);
+            v[4 * t + 2] = __builtin_bit_cast(float, xraw[t].z);
+            v[4 * t + 3] = __builtin_bit_cast(float, xraw[t].w);
+        }
+        if (a.gamma) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float gm[4] = {__builtin_bit_cast(float, graw[t].x), __builtin_bit_cast(float, graw[t].y),
+                                     __builtin_bit_cast(float, graw[t].z), __builtin_bit_cast(float, graw[t].w)};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ssq = fmaf(v[4 * t + e], v[4 * t + e], ssq);
+                    v[4 * t + e] *= gm[e];
+                }
+            }
+        }
+        uint32_t p[16], lo[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float u = v[8 * j + q], w = v[8 * j + q + 4];
+                const _Float16 hu = (_Float16)u, hw = (_Float16)w;
+                const _Float16 lu = (_Float16)(u - (float)hu), lw = (_Float16)(w - (float)hw);
+                p[4 * j + q] = (uint32_t)h_bits(hu) | ((uint32_t)h_bits(hw) << 16);
+                lo[4 * j + q] = (uint32_t)h_bits(lu) | ((uint32_t)h_bits(lw) << 16);
+            }
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) s += v[t];
+        uint4* dh = reinterpret_cast<uint4*>(xh + idx * 16);
+        uint4* dl = reinterpret_cast<uint4*>(xl + idx * 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            dh[t] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
+            dl[t] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
+        }
+        sums[idx] = s;
+    };
+    stage_chunk(tid, xraw, graw);
+    if (G > 256) {  // K > 8192: a second chunk per thread (G <= 512)
+        load_chunk(tid + 256, xraw, graw);
+        stage_chunk(tid + 256, xraw, graw);
+    }
+    ssq_part[tid] = ssq;
+    __syncthreads();
+    if (!live) return;
+
+    // norm factor: the 256 partials in a fixed order (lane l adds l, l + 64, l + 128, l + 192)
+    float inv = 1.0f;
+    if (a.gamma) {
+        const float t = (ssq_part[lane] + ssq_part[lane + 64]) + (ssq_part[lane + 128] + ssq_part[lane + 192]);
+        const float total = wave_sum_lane63(t);
+        inv = 1.0f / sqrtf(total / (float)K + a.eps);  // meaningful on lane 63, which stores
+    }
+
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
+    const h2 bias_lo = {1024, 1024}, bias_hi = {64, 64};
+
+    // 5. chunks in load order, each chunk's input pairs read from LDS once for all the wave's rows;
+    // then the wave sums (lane 63) and the epilogue on lane 63
+    float dots[NM][R];
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+        const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = (int)(coff[c] >> 4);
+            uint32_t xp[16], xq[16];
+            const uint4* sh = reinterpret_cast<const uint4*>(xh + idx * 16);
+            const uint4* sl = reinterpret_cast<const uint4*>(xl + idx * 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint4 u = sh[t], w = sl[t];
+                xp[4 * t] = u.x; xp[4 * t + 1] = u.y; xp[4 * t + 2] = u.z; xp[4 * t + 3] = u.w;
+                xq[4 * t] = w.x; xq[4 * t + 1] = w.y; xq[4 * t + 2] = w.z; xq[4 * t + 3] = w.w;
+            }
+            const float sxc = sums[idx];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t dw[4] = {wv[j][r][c].x, wv[j][r][c].y, wv[j][r][c].z, wv[j][r][c].w};
+                float p = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t d8 = dw[w] >> 8;
+                    const h2 q0 = bits_h2((dw[w] & 0x000F000Fu) | mag_lo) - bias_lo;
+                    const h2 q1 = bits_h2((dw[w] & 0x00F000F0u) | mag_hi) - bias_hi;
+                    const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo) - bias_lo;
+                    const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi) - bias_hi;
+                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 0]), q0, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 0]), q0, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 1]), q1, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 1]), q1, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 2]), q2, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 2]), q2, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 3]), q3, p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 3]), q3, p, false);
+                }
+                float sc = SF16 ? (float)bits_h((uint16_t)sraw[j][r][c]) : __builtin_bit_cast(float, sraw[j][r][c]);
+                sc = cv[c] ? sc : 0.0f;
+                const float z = ZU ? fm.zero_value : __builtin_bit_cast(float, zraw[j][r][c]);
+                acc[r] = fmaf(sc, p - z * sxc, acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) dots[j][r] = wave_sum_lane63(acc[r]);
+    }
+    if (lane == 63) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = n0 + r;
+            if (row >= fm0.N) continue;
+            float v = dots[0][r] * inv;
+            if constexpr (MODE == 1) {
+                const float u = dots[1][r] * inv;
+                v = v / (1.0f + expf(-v)) * u;
+            }
+            if (a.res) v += a.res[row];
+            fm0.y[row] = v;
+        }
+    }
+}
+
+template <int CPL, int MODE>
+void launch_fused_sz(const FusedArgs& a, bool sf16, bool zu) {
+    const int G = a.K / 32;
+    const size_t lds = (size_t)G * 16 * 4 * 2 + (size_t)G * 4 + 256 * 4;
+    const dim3 grid((a.batches + 3) / 4);
+#define BYHIP_FUSED_CASE(SF, ZU_) \
+    if (sf16 == SF && zu == ZU_) { hipLaunchKernelGGL((q4_gemv_fused<CPL, SF, ZU_, MODE>), grid, dim3(256), lds, stream(), a); }
+    BYHIP_FUSED_CASE(true, true)
+    else BYHIP_FUSED_CASE(true, false)
+    else BYHIP_FUSED_CASE(false, true)
+    else BYHIP_FUSED_CASE(false, false)
+#undef BYHIP_FUSED_CASE
+    BYHIP_LAUNCHED("q4_gemv_fused");
+}
+
 }  // namespace
 
 bool q4_gemv_eligible(const byhip_q4w* w, int M, int x_dtype) {
@@ -421,6 +698,58 @@ void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
             default: launch_cpl<4, false>(cpl, a, w, blk, y_dtype); break;
             }
         }
+    }
+}
+
+
+int q4_fused_check(int mode, const byhip_q4w* const* ws, int n_ws) {
+    if (mode != 0 && mode != 1) return BYHIP_UNSUPPORTED;
+    if (n_ws < 1 || n_ws > 3 || (mode == 1 && n_ws != 2)) return BYHIP_UNSUPPORTED;
+    const byhip_q4w* w0 = ws[0];
+    for (int i = 0; i < n_ws; ++i) {
+        const byhip_q4w* w = ws[i];
+        if (!w) return BYHIP_UNSUPPORTED;
+        if (w->K != w0->K || w->group != w0->group || w->gpr != w0->gpr) return BYHIP_UNSUPPORTED;
+        if (!w->sblk || w->blk_scale_f16 != w0->blk_scale_f16 || w->zero_uniform != w0->zero_uniform)
+            return BYHIP_UNSUPPORTED;
+        // 32-bit buffer offsets for weights and the blocked scales, 16-byte aligned rows
+        const uint64_t lim = kOutOfRange - 64;
+        if ((uint64_t)w->N * w->row_bytes >= lim || (uint64_t)(w->N + 8) * (w->K / 32) * 4 >= lim ||
+            reinterpret_cast<uintptr_t>(w->wq) % 16 != 0)
+            return BYHIP_UNSUPPORTED;
+    }
+    if (w0->K % 32 != 0 || (w0->group != 0 && w0->group % 32 != 0)) return BYHIP_UNSUPPORTED;
+    if (mode == 1 && ws[1]->N != w0->N) return BYHIP_UNSUPPORTED;
+    // chunks per lane: 8 at most (4 with gate and up); the staged input fits 64 KB of LDS
+    const int G = w0->K / 32;
+    if (gemv_cpl(w0->K) > (mode == 1 ? 4 : 8) || (size_t)G * 132 + 1024 > 65536) return BYHIP_UNSUPPORTED;
+    return BYHIP_OK;
+}
+
+void launch_q4_gemv_fused(int mode, const float* x, const byhip_q4w* const* ws, int n_ws, float* const* outs,
+                          const float* res, const float* gamma, float eps) {
+    FusedArgs a{};
+    const int cpl = gemv_cpl(ws[0]->K);
+    const int rows = fused_rows(cpl);
+    a.x = x; a.res = res; a.gamma = gamma; a.eps = eps;
+    a.K = ws[0]->K; a.row_bytes = (int)ws[0]->row_bytes; a.nmats = n_ws;
+    int batches = 0;
+    for (int i = 0; i < n_ws; ++i) {
+        const byhip_q4w* w = ws[i];
+        FusedMat& m = a.m[i];
+        m.wq = w->wq; m.sblk = w->sblk; m.zblk = w->zblk; m.zero_value = w->zero_value;
+        m.y = mode == 1 ? outs[0] : outs[i];
+        m.N = w->N; m.n_pad = (w->N + 7) / 8 * 8;
+        m.batch0 = mode == 1 ? 0 : batches;
+        if (mode == 0 || i == 0) batches += (w->N + rows - 1) / rows;
+    }
+    a.batches = batches;
+    const bool sf = ws[0]->blk_scale_f16, zu = ws[0]->zero_uniform;
+    switch (cpl) {
+    case 1: mode ? launch_fused_sz<1, 1>(a, sf, zu) : launch_fused_sz<1, 0>(a, sf, zu); break;
+    case 2: mode ? launch_fused_sz<2, 1>(a, sf, zu) : launch_fused_sz<2, 0>(a, sf, zu); break;
+    case 4: mode ? launch_fused_sz<4, 1>(a, sf, zu) : launch_fused_sz<4, 0>(a, sf, zu); break;
+    default: launch_fused_sz<8, 0>(a, sf, zu); break;  // mode 1 stops at 4 (q4_fused_check)
     }
 }
 

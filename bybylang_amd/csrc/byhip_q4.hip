@@ -374,6 +374,38 @@ int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
     });
 }
 
+int byhip_q4_matmul_fused(int mode, const float* a, byhip_q4w* const* ws, int n_ws, float* const* outs,
+                          int n_outs, const float* res, int has_res, const float* gamma, float eps,
+                          int has_norm) {
+    return guard([&] {
+        enter_compute();
+        if (!a) fail("byhip: null fused GEMV input");
+        if (!ws || !outs) unsupported("byhip: fused GEMV without weights or outputs");
+        // The reference's encoders return false for these (gpubackend.nim:3200-3206, 3219-3225).
+        if (n_ws < 1 || n_ws > 3 || n_outs < n_ws || (mode == 1 && n_ws != 2) || (mode != 0 && mode != 1))
+            unsupported("byhip: fused GEMV takes 1..3 weights in mode 0, gate and up in mode 1 (mode=%d, %d weights, %d outputs)",
+                        mode, n_ws, n_outs);
+        if (has_res && !res) unsupported("byhip: fused GEMV residual requested without a buffer");
+        if (has_norm && !gamma) unsupported("byhip: fused GEMV norm requested without weights");
+        // The reference wants an allocated output per weight, also in mode 1, where only outs[0]
+        // is written (gpubackend.nim:3204-3206).
+        for (int i = 0; i < n_ws; ++i)
+            if (!outs[i]) unsupported("byhip: fused GEMV output %d is not allocated", i);
+        const int n_out = mode == 1 ? 1 : n_ws;
+        if (q4_fused_check(mode, ws, n_ws) != BYHIP_OK)
+            unsupported("byhip: fused GEMV does not take these weights (K, group, groups per row and "
+                        "scale formats must match, K %% 32 == 0, K <= 8192, equal N for gate and up)");
+        const int K = ws[0]->K;
+        int max_n = 0;
+        for (int i = 0; i < n_ws; ++i) max_n = std::max(max_n, ws[i]->N);
+        check_span(a, (size_t)K * 4, "fused GEMV input");
+        for (int i = 0; i < n_out; ++i) check_span(outs[i], (size_t)ws[i]->N * 4, "fused GEMV output");
+        if (has_res) check_span(res, (size_t)(mode == 1 ? ws[0]->N : max_n) * 4, "fused GEMV residual");
+        if (has_norm) check_span(gamma, (size_t)K * 4, "fused GEMV norm weights");
+        launch_q4_gemv_fused(mode, a, ws, n_ws, outs, has_res ? res : nullptr, has_norm ? gamma : nullptr, eps);
+    });
+}
+
 int byhip_gpu_matmul_q4(const float* a, const uint8_t* wq, const float* scales, const float* zeros,
                         float* c, int M, int K, int N, int group_size, int groups_per_row) {
     return guard([&] {

@@ -142,6 +142,21 @@ def q4_matmul(x: DeviceBuffer, x_dtype: int, w: Q4Weights, y: DeviceBuffer, y_dt
     check(load().byhip_q4_matmul(x.ptr, x_dtype, w.handle, y.ptr, y_dtype, M), "byhip_q4_matmul")
 
 
+def q4_matmul_fused(mode: int, a: DeviceBuffer, ws, outs, res: DeviceBuffer = None,
+                    gamma: DeviceBuffer = None, eps: float = 0.0) -> int:
+    """The fused decode GEMV (byhip_q4_matmul_fused): returns BYHIP_OK, or BYHIP_UNSUPPORTED when
+    the library does not take the combination (the caller then runs the unfused sequence)."""
+    wp = (C.c_void_p * max(1, len(ws)))(*[w.handle for w in ws])
+    op = (C.c_void_p * max(1, len(outs)))(*[o.ptr for o in outs])
+    rc = load().byhip_q4_matmul_fused(mode, a.ptr, C.cast(wp, C.c_void_p), len(ws), C.cast(op, C.c_void_p),
+                                      len(outs), res.ptr if res is not None else None, int(res is not None),
+                                      gamma.ptr if gamma is not None else None, eps, int(gamma is not None))
+    if rc == _abi.BYHIP_UNSUPPORTED:
+        return rc
+    check(rc, "byhip_q4_matmul_fused")
+    return rc
+
+
 def fp4km_tile_gemm(x: DeviceBuffer, x_dtype: int, blob: DeviceBuffer, scale_base: int,
                     lut: DeviceBuffer, lut_base: int, y: DeviceBuffer, y_dtype: int,
                     M: int, K: int, N: int) -> None:

@@ -257,6 +257,37 @@ def sessionMatmulQ4(backend: GpuBackend, a: SessionHandle, w: ResidentWeightHand
     return True
 
 
+def sessionMatmulQ4Fused(backend: GpuBackend, mode: int, a: SessionHandle, ws, outs,
+                         res: SessionHandle, hasRes: bool, gamma: SessionHandle = None,
+                         eps: float = 0.0, hasNorm: bool = False) -> bool:
+    """sessionMatmulQ4Fused, gpubackend.nim:3185-3231: the fused decode GEMV (M = 1). mode 0: ws
+    (1..3 resident weights) share a, outs[i] receives ws[i]; mode 1: ws = [gate, up], outs[0] =
+    silu(gate . x) * (up . x). res is added when hasRes; with hasNorm, a is the raw vector and
+    RMSNorm (gamma, eps) is applied inside the kernel. Output handles must already be allocated.
+    Returns False when unsupported, so callers run the unfused sequence."""
+    import ctypes as C
+    _require_hip(backend)
+    if a.hipHandle is None or len(ws) < 1 or len(ws) > 3 or len(outs) < len(ws) or \
+            (mode == 1 and len(ws) != 2):
+        return False
+    if hasRes and (res is None or res.hipHandle is None):
+        return False
+    if hasNorm and (gamma is None or gamma.hipHandle is None):
+        return False
+    if any(w.hipWeights is None for w in ws) or any(o.hipHandle is None for o in outs[:len(ws)]):
+        return False
+    wp = (C.c_void_p * len(ws))(*[w.hipWeights for w in ws])
+    op = (C.c_void_p * len(outs))(*[o.hipHandle for o in outs])
+    rc = load().byhip_q4_matmul_fused(mode, a.hipHandle, C.cast(wp, C.c_void_p), len(ws),
+                                      C.cast(op, C.c_void_p), len(outs),
+                                      res.hipHandle if hasRes else None, int(hasRes),
+                                      gamma.hipHandle if hasNorm else None, eps, int(hasNorm))
+    if rc == _abi.BYHIP_UNSUPPORTED:
+        return False
+    check(rc, "sessionMatmulQ4Fused")
+    return True
+
+
 def gpuMatmulQ4(backend: GpuBackend, a, wq, scales, zeros, m: int, k: int, n: int, groupSize: int,
                 nGroupsPerRow: int, cpuFallback=None) -> np.ndarray:
     """gpuMatmulQ4, gpubackend.nim:806-843: host fp32 in and out, weights uploaded per call.

@@ -164,6 +164,25 @@ int byhip_q4_resident_info(const byhip_q4w* w, byhip_q4w_info* out);
  * cpu_vm.c:420-482) with fp32 accumulation. x_dtype: BYHIP_F32 or BYHIP_F16; y_dtype: BYHIP_F32,
  * BYHIP_F16 or BYHIP_BF16. M <= 8 runs the decode GEMV, larger M the MFMA GEMM. */
 int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
+
+/* sessionMatmulQ4Fused (gpubackend.nim:3185-3231; its shader, q4_autotune.nim:194-330): the fused
+ * decode GEMV, M = 1, on fp32 device buffers.
+ *   mode 0: ws[0..n_ws-1] (1..3 resident weights of equal K, group and groups per row) share `a`
+ *           (K floats); outs[i] receives ws[i]'s N rows.
+ *   mode 1: ws = {gate, up} of equal N; outs[0][row] = silu(gate . x) * (up . x), with
+ *           silu(v) = v / (1 + exp(-v)). As in the reference, outs holds an allocated buffer per
+ *           weight (n_outs >= 2); only outs[0] is written.
+ *   has_norm: `a` is the raw vector; RMSNorm with weights `gamma` (K floats) and `eps` is applied
+ *           inside the kernel: x = a * gamma, each dot product times 1 / sqrt(sum a^2 / K + eps).
+ *   has_res: res[row] (matrix-local row) is added to each output.
+ * Returns BYHIP_UNSUPPORTED, with the outputs untouched, for the combinations the reference's
+ * encoders reject (n_ws outside 1..3, n_outs < n_ws, mode 1 without exactly two weights, a missing
+ * output, residual or norm buffer) and for weights this kernel does not take (mismatched shapes
+ * or scale formats, K % 32 != 0, K > 8192): the caller then runs the unfused sequence, as the
+ * reference's callers do. */
+int byhip_q4_matmul_fused(int mode, const float* a, byhip_q4w* const* ws, int n_ws, float* const* outs,
+                          int n_outs, const float* res, int has_res, const float* gamma, float eps,
+                          int has_norm);
 /* gpuMatmulQ4 (gpubackend.nim:806-843): host fp32 in, host fp32 out; uploads the weights on every
  * call and waits, like vulkanMatmulQ4 (vulkan_driver.nim:1012-1161). */
 int byhip_gpu_matmul_q4(const float* a, const uint8_t* wq, const float* scales, const float* zeros,

@@ -8,6 +8,7 @@
 #include "byby_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -289,6 +290,62 @@ void orc_matmul_q4(const float* a, const uint8_t* wq, const float* scales, const
             c[(size_t)m * N + n] = sum;
         }
     }
+}
+
+/* sessionMatmulQ4Fused (gpubackend.nim:3185-3231), shader q4_autotune.nim:194-330. */
+static float fused_row_dot(const float* x, const uint8_t* wq, const float* scales, const float* zeros,
+                           int row, int K, int group_size, int groups_per_row) {
+    const uint8_t* wrow = wq + (size_t)row * (size_t)((K + 1) / 2);
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const int gi = row * groups_per_row + (group_size > 0 ? k / group_size : 0);
+        const uint8_t byte = wrow[k >> 1];
+        const uint8_t nib = (k & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0x0F);
+        const float w = ((float)nib - zeros[gi]) * scales[gi];
+        acc = fmaf(w, x[k], acc);
+    }
+    return acc;
+}
+
+int orc_q4_fused(int mode, int n_mats, const float* a, int K, int group_size, int groups_per_row,
+                 const uint8_t* const* wq, const float* const* scales, const float* const* zeros,
+                 const int* N, float* const* out, const float* residual, const float* gamma,
+                 float eps) {
+    if (n_mats < 1 || n_mats > 3 || (mode == 1 && n_mats != 2) || (mode != 0 && mode != 1))
+        return -1;
+    float* x = (float*)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+    if (!x) return -1;
+    float ssq = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        if (gamma) {
+            ssq = fmaf(a[k], a[k], ssq);
+            x[k] = a[k] * gamma[k];
+        } else {
+            x[k] = a[k];
+        }
+    }
+    const float inv = gamma ? 1.0f / sqrtf(ssq / (float)K + eps) : 1.0f;
+    if (mode == 0) {
+        for (int i = 0; i < n_mats; ++i)
+            for (int row = 0; row < N[i]; ++row) {
+                float v = fused_row_dot(x, wq[i], scales[i], zeros[i], row, K, group_size,
+                                        groups_per_row) * inv;
+                if (residual) v += residual[row];
+                out[i][row] = v;
+            }
+    } else {
+        for (int row = 0; row < N[0]; ++row) {
+            const float g = fused_row_dot(x, wq[0], scales[0], zeros[0], row, K, group_size,
+                                          groups_per_row) * inv;
+            const float u = fused_row_dot(x, wq[1], scales[1], zeros[1], row, K, group_size,
+                                          groups_per_row) * inv;
+            float v = g / (1.0f + expf(-g)) * u;
+            if (residual) v += residual[row];
+            out[0][row] = v;
+        }
+    }
+    free(x);
+    return 0;
 }
 
 /* gpubackend.nim:288-311. */

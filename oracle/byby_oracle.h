@@ -84,6 +84,22 @@ void orc_matmul_q4(const float* a, const uint8_t* wq, const float* scales, const
 void orc_matmul_q4_ref(const float* a, const uint8_t* wq, const float* scales, const float* zeros,
                        float* c, int M, int K, int N, int group_size, int groups_per_row);
 
+/* The fused decode GEMV (M = 1) of sessionMatmulQ4Fused (gpubackend.nim:3185-3231) with the
+ * arithmetic of its shader matmul_q4_fused (backends/vulkan/q4_autotune.nim:194-330):
+ *   x[k] = a[k] * gamma[k] with RMSNorm (gamma != NULL), else a[k];
+ *   per output row: acc = sum over k of fma(w, x[k], acc), w = ((float)q - z) * s;
+ *   with RMSNorm, acc *= inv, inv = 1 / sqrt(ssq / K + eps), ssq = sum of fma(a, a, ssq);
+ *   mode 0: n_mats (1..3) matrices share x, out[i][row] = acc_i;
+ *   mode 1: matrices 0 (gate) and 1 (up), out[0][row] = silu(g) * u, silu(v) = v / (1 + exp(-v));
+ *   residual[row] (matrix-local row) is added last when residual != NULL.
+ * Sums run over k in order (the shader's lane partition and tree reduction reorder them; the
+ * checks allow fp32 accumulation differences). Returns 0, or -1 for the argument combinations the
+ * reference rejects (n_mats outside 1..3, mode 1 without exactly two matrices, another mode). */
+int orc_q4_fused(int mode, int n_mats, const float* a, int K, int group_size, int groups_per_row,
+                 const uint8_t* const* wq, const float* const* scales, const float* const* zeros,
+                 const int* N, float* const* out, const float* residual, const float* gamma,
+                 float eps);
+
 /* A shape-op program run the way nimf_cpu_vm_run_slots (cpu_vm.c:178) runs it: the first
  * instruction is one of the five-word shape ops, the rest may only be the tile ops (no-ops on the
  * CPU, cpu_vm.c:629-631), threadgroup barriers, NOPs and HALT. Slot lengths are in the units the

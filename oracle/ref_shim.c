@@ -1,9 +1,10 @@
-/* ref_shim.c - exports two entry points of the reference's CPU backend for the checker.
+/* ref_shim.c - exports three entry points of the reference's CPU backend for the checker.
  *
  * TEST INFRASTRUCTURE ONLY. The reference declares its kernels with hidden visibility
  * (backends/cpu/cpu_kernels.h:16-18, 86, 118), so a shared object built from its sources exports
  * nothing; this file is linked into that same object (oracle/_ref/libbybyref.so) and forwards to
- * the two functions the quantized tile-GEMM path uses. It contains no arithmetic of its own.
+ * the two functions the quantized tile-GEMM path uses, and to the RMSNorm of the unfused sequence
+ * that the fused decode GEMV replaces. It contains no arithmetic of its own.
  */
 #include "cpu_kernels.h"
 
@@ -21,4 +22,8 @@ REFSHIM_EXPORT int refshim_vm_run_slots(uint32_t* code, int n_words, float* mem,
 REFSHIM_EXPORT void refshim_matmul_q4(float* a, uint8_t* wq, float* scales, float* zeros, float* c,
                                       int M, int K, int N, int group_size, int groups_per_row) {
     nimf_cpu_matmul_q4(a, wq, scales, zeros, c, M, K, N, group_size, groups_per_row);
+}
+
+REFSHIM_EXPORT void refshim_rmsnorm(float* x, float* gamma, float* out, int rows, int cols, float eps) {
+    nimf_cpu_rmsnorm(x, gamma, out, rows, cols, eps);
 }

@@ -134,6 +134,10 @@ class Oracle:
         L.orc_make_f16_case.restype = None
         L.orc_make_f16_case.argtypes = [C.POINTER(C.c_uint32), C.c_int, C.c_int, C.c_int,
                                         C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_q4_fused.restype = C.c_int
+        L.orc_q4_fused.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                   C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                   C.c_void_p, C.c_void_p, C.c_float]
 
     # -- conversions
     def half_to_float(self, h: int) -> float:
@@ -195,6 +199,28 @@ class Oracle:
                                  group, groups_per_row)
         return c.reshape(M, N)
 
+    def q4_fused(self, mode, a, mats, K, group, groups_per_row, residual=None, gamma=None, eps=0.0):
+        """mats: list of (wq, scales, zeros, N). Returns the list of outputs (one in mode 1), or
+        None when the reference rejects the combination."""
+        n = len(mats)
+        keep = [np.ascontiguousarray(m[0]) for m in mats] + [np.ascontiguousarray(m[1], np.float32) for m in mats] + \
+            [np.ascontiguousarray(m[2], np.float32) for m in mats]
+        wq = (C.c_void_p * max(n, 1))(*[_ptr(keep[i]) for i in range(n)])
+        sc = (C.c_void_p * max(n, 1))(*[_ptr(keep[n + i]) for i in range(n)])
+        ze = (C.c_void_p * max(n, 1))(*[_ptr(keep[2 * n + i]) for i in range(n)])
+        Ns = (C.c_int * max(n, 1))(*[int(m[3]) for m in mats])
+        outs = [np.zeros(int(m[3]), dtype=np.float32) for m in mats]
+        op = (C.c_void_p * max(n, 1))(*[_ptr(o) for o in outs])
+        a = np.ascontiguousarray(a, np.float32)
+        res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+        gam = None if gamma is None else np.ascontiguousarray(gamma, np.float32)
+        rc = self.L.orc_q4_fused(mode, n, _ptr(a), K, group, groups_per_row, C.cast(wq, C.c_void_p),
+                                 C.cast(sc, C.c_void_p), C.cast(ze, C.c_void_p), C.cast(Ns, C.c_void_p),
+                                 C.cast(op, C.c_void_p), _ptr(res), _ptr(gam), eps)
+        if rc != 0:
+            return None
+        return outs[:1] if mode == 1 else outs
+
     def unpack_q4(self, wq, K, N):
         codes = np.zeros(N * K, dtype=np.uint8)
         self.L.orc_unpack_q4(_ptr(wq), K, N, _ptr(codes))
@@ -223,7 +249,8 @@ class Oracle:
 
 
 class Reference:
-    """oracle/_ref/libbybyref.so: nimf_cpu_vm_run_slots and nimf_cpu_matmul_q4 of the reference."""
+    """oracle/_ref/libbybyref.so: nimf_cpu_vm_run_slots, nimf_cpu_matmul_q4 and nimf_cpu_rmsnorm of
+    the reference."""
 
     def __init__(self, path: str = REF_SO):
         L = C.CDLL(path)
@@ -234,6 +261,8 @@ class Reference:
                                            C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_int]
         L.refshim_matmul_q4.restype = None
         L.refshim_matmul_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 5
+        L.refshim_rmsnorm.restype = None
+        L.refshim_rmsnorm.argtypes = [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_float]
 
     @staticmethod
     def available() -> bool:
@@ -256,6 +285,14 @@ class Reference:
         self.L.refshim_matmul_q4(_ptr(a), _ptr(wq), _ptr(scales), _ptr(zeros), _ptr(c), M, K, N,
                                  group, groups_per_row)
         return c.reshape(M, N)
+
+
+    def rmsnorm(self, x, gamma, rows, cols, eps):
+        x = np.ascontiguousarray(x, np.float32).copy()  # the reference takes mutable pointers
+        gamma = np.ascontiguousarray(gamma, np.float32).copy()
+        out = np.zeros(rows * cols, dtype=np.float32)
+        self.L.refshim_rmsnorm(_ptr(x), _ptr(gamma), _ptr(out), rows, cols, eps)
+        return out
 
 
 def fp4_cases(oracle: Oracle):
