@@ -76,50 +76,57 @@ __global__ void q4_unpack(const uint8_t* __restrict__ wq, size_t row_bytes, int 
     }
 }
 
-// ── host side ───────────────────────────────────────────────────────────────────────────────
-
-// binary32 -> binary16 round to nearest even, on the host (scale classification).
-uint16_t host_f32_to_f16(float f) {
-    uint32_t x;
-    memcpy(&x, &f, 4);
-    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
-    const uint32_t ax = x & 0x7FFFFFFFu;
-    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
-    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
-    if (ax < 0x38800000u) {
-        if (ax < 0x33000000u) return sign;
-        const uint32_t e = ax >> 23, m = (ax & 0x7FFFFFu) | 0x800000u, sh = 126u - e;
-        uint32_t q = m >> sh;
-        const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
-        if (rem > half || (rem == half && (q & 1u))) ++q;
-        return (uint16_t)(sign | q);
+// Classification of the scales and zeros of a resident upload, per block: flags[2b] = every
+// scale in the block is finite and converts to fp16 exactly, flags[2b + 1] = every zero equals
+// zeros[0] bit for bit. The host ANDs the block flags.
+__global__ __launch_bounds__(256) void q4_classify(const float* __restrict__ sc, const float* __restrict__ ze,
+                                                   size_t ng, int* __restrict__ flags) {
+    const uint32_t z0 = __builtin_bit_cast(uint32_t, ze[0]);
+    int ok_s = 1, ok_z = 1;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < ng; i += (size_t)gridDim.x * 256) {
+        const float s = sc[i];
+        ok_s &= (__builtin_isfinite(s) && (float)(_Float16)s == s) ? 1 : 0;
+        ok_z &= __builtin_bit_cast(uint32_t, ze[i]) == z0 ? 1 : 0;
     }
-    uint32_t q = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
-    const uint32_t rem = ax & 0x1FFFu;
-    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;
-    return (uint16_t)(sign | q);
+    ok_s = __syncthreads_and(ok_s);
+    ok_z = __syncthreads_and(ok_z);
+    if (threadIdx.x == 0) {
+        flags[2 * blockIdx.x] = ok_s;
+        flags[2 * blockIdx.x + 1] = ok_z;
+    }
 }
 
-float host_f16_to_f32(uint16_t h) {
-    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, bits;
-    if (e == 0) {
-        if (m == 0) {
-            bits = sign;
-        } else {
-            e = 113;
-            while (!(m & 0x400u)) { m <<= 1; --e; }
-            bits = sign | (e << 23) | ((m & 0x3FFu) << 13);
+// The resident scale and zero layouts from fp32 device arrays [N * gpr]: plain scales (fp16 when
+// sf16), plain zeros (unless uniform), and the decode copy [ceil(N/8)][K/32][8] (padded rows 0).
+__global__ __launch_bounds__(256) void q4_pack_scales(const float* __restrict__ sc, const float* __restrict__ ze,
+                                                      int N, int gpr, int group, int G, int sf16, int zu,
+                                                      void* __restrict__ scales, float* __restrict__ zeros,
+                                                      void* __restrict__ sblk, float* __restrict__ zblk) {
+    const size_t ng = (size_t)N * gpr, nb = sblk ? (size_t)(N + 7) / 8 * 8 * G : 0;
+    const size_t total = ng > nb ? ng : nb;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        if (i < ng) {
+            if (sf16) static_cast<_Float16*>(scales)[i] = (_Float16)sc[i];
+            else static_cast<float*>(scales)[i] = sc[i];
+            if (!zu) zeros[i] = ze[i];
         }
-    } else if (e == 31) {
-        bits = sign | 0x7F800000u | (m << 13);
-    } else {
-        bits = sign | ((e + 112u) << 23) | (m << 13);
+        if (i < nb) {
+            // entry i = ((n / 8) * G + ch) * 8 + n % 8
+            const size_t n = (i / ((size_t)G * 8)) * 8 + i % 8, ch = (i / 8) % G;
+            float s = 0.0f, z = 0.0f;
+            if (n < (size_t)N) {
+                const size_t src = n * gpr + (group ? ch * 32 / (size_t)group : 0);
+                s = sc[src];
+                z = ze[src];
+            }
+            if (sf16) static_cast<_Float16*>(sblk)[i] = (_Float16)s;
+            else static_cast<float*>(sblk)[i] = s;
+            if (!zu) zblk[i] = z;
+        }
     }
-    float f;
-    memcpy(&f, &bits, 4);
-    return f;
 }
+
+// ── host side ───────────────────────────────────────────────────────────────────────────────
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -131,17 +138,34 @@ void validate_q4_shape(int K, int N, int group, int gpr) {
         fail("byhip: K=%d with group_size %d needs %d groups per row, got %d", K, group, used, gpr);
 }
 
-byhip_q4w* build_resident(const uint8_t* wq_rows, const float* scales, const float* zeros, int K,
-                          int N, int group, int gpr) {
+// The resident layout from nibble rows at wq_src (host memory, or device memory when wq_on_device)
+// and fp32 scales / zeros [N * gpr] in device memory. The scale format and the uniform zero are
+// decided on the device (q4_classify) and the layouts written there (q4_pack_scales), so the host
+// does no per-element work; only the block flags and zeros[0] come back.
+byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float* d_sc, const float* d_ze,
+                              int K, int N, int group, int gpr) {
     const size_t row_bytes = (size_t)(K + 1) / 2;
     const size_t ng = (size_t)N * gpr;
-    bool sf16 = true;
-    for (size_t i = 0; i < ng && sf16; ++i) {
-        const float s = scales[i];
-        sf16 = std::isfinite(s) && host_f16_to_f32(host_f32_to_f16(s)) == s;
+    const int cblocks = (int)std::min<size_t>((ng + 255) / 256, 1024);
+    int* d_flags = static_cast<int*>(device_alloc((size_t)cblocks * 2 * sizeof(int)));
+    std::vector<int> flags((size_t)cblocks * 2);
+    float zero0 = 0.0f;
+    try {
+        hipLaunchKernelGGL(q4_classify, dim3(cblocks), dim3(256), 0, stream(), d_sc, d_ze, ng, d_flags);
+        BYHIP_LAUNCHED("q4_classify");
+        BYHIP_HIP(hipMemcpyAsync(flags.data(), d_flags, flags.size() * sizeof(int), hipMemcpyDeviceToHost, stream()));
+        BYHIP_HIP(hipMemcpyAsync(&zero0, d_ze, sizeof(float), hipMemcpyDeviceToHost, stream()));
+        BYHIP_HIP(hipStreamSynchronize(stream()));
+    } catch (...) {
+        device_free(d_flags);
+        throw;
     }
-    bool zu = true;
-    for (size_t i = 1; i < ng && zu; ++i) zu = memcmp(&zeros[i], &zeros[0], 4) == 0;
+    device_free(d_flags);
+    bool sf16 = true, zu = true;
+    for (int b = 0; b < cblocks; ++b) {
+        sf16 = sf16 && flags[2 * b];
+        zu = zu && flags[2 * b + 1];
+    }
     const size_t wq_bytes = (size_t)N * row_bytes;
     const size_t s_bytes = ng * (sf16 ? 2 : 4);
     const size_t z_bytes = zu ? 0 : ng * 4;
@@ -160,44 +184,43 @@ byhip_q4w* build_resident(const uint8_t* wq_rows, const float* scales, const flo
     w->zeros = zu ? nullptr : reinterpret_cast<float*>(base + o_z);
     w->scale_f16 = sf16;
     w->zero_uniform = zu;
-    w->zero_value = zu ? zeros[0] : 0.0f;
+    w->zero_value = zu ? zero0 : 0.0f;
     w->bytes = total;
     w->sblk = blk ? base + o_sb : nullptr;
     w->zblk = blk && !zu ? reinterpret_cast<float*>(base + o_zb) : nullptr;
     w->blk_scale_f16 = sf16;
     try {
-        BYHIP_HIP(hipMemcpyAsync(w->wq, wq_rows, wq_bytes, hipMemcpyHostToDevice, stream()));
-        std::vector<uint16_t> h;
-        if (sf16) {
-            h.resize(ng);
-            for (size_t i = 0; i < ng; ++i) h[i] = host_f32_to_f16(scales[i]);
-            BYHIP_HIP(hipMemcpyAsync(w->scales, h.data(), s_bytes, hipMemcpyHostToDevice, stream()));
-        } else {
-            BYHIP_HIP(hipMemcpyAsync(w->scales, scales, s_bytes, hipMemcpyHostToDevice, stream()));
-        }
-        if (!zu) BYHIP_HIP(hipMemcpyAsync(w->zeros, zeros, z_bytes, hipMemcpyHostToDevice, stream()));
-        std::vector<uint8_t> sb(sb_bytes, 0), zb(zb_bytes, 0);
-        if (blk) {
-            // entry (n, chunk) of the decode copy: [(n / 8) * G + chunk] * 8 + n % 8; padded rows are 0
-            for (size_t n = 0; n < (size_t)N; ++n)
-                for (size_t ch = 0; ch < G; ++ch) {
-                    const size_t g = group ? ch * 32 / (size_t)group : 0;
-                    const size_t src = n * gpr + g, dst = ((n / 8) * G + ch) * 8 + n % 8;
-                    if (sf16)
-                        memcpy(&sb[dst * 2], &h[src], 2);
-                    else
-                        memcpy(&sb[dst * 4], &scales[src], 4);
-                    if (!zu) memcpy(&zb[dst * 4], &zeros[src], 4);
-                }
-            BYHIP_HIP(hipMemcpyAsync(w->sblk, sb.data(), sb_bytes, hipMemcpyHostToDevice, stream()));
-            if (!zu) BYHIP_HIP(hipMemcpyAsync(w->zblk, zb.data(), zb_bytes, hipMemcpyHostToDevice, stream()));
-        }
-        BYHIP_HIP(hipStreamSynchronize(stream()));
+        BYHIP_HIP(hipMemcpyAsync(w->wq, wq_src, wq_bytes, wq_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                 stream()));
+        const size_t work = std::max(ng, blk ? n_pad * G : (size_t)0);
+        const int pblocks = (int)std::min<size_t>((work + 255) / 256, (size_t)compute_units() * 16);
+        hipLaunchKernelGGL(q4_pack_scales, dim3(pblocks), dim3(256), 0, stream(), d_sc, d_ze, N, gpr, group, (int)G,
+                           (int)sf16, (int)zu, w->scales, w->zeros, w->sblk, w->zblk);
+        BYHIP_LAUNCHED("q4_pack_scales");
+        BYHIP_HIP(hipStreamSynchronize(stream()));  // the source may be pageable host memory
     } catch (...) {
         device_free(base);
         delete w;
         throw;
     }
+    return w;
+}
+
+// The same from host scale and zero arrays: they go to the device as they are, then as above.
+byhip_q4w* build_resident(const uint8_t* wq_rows, const float* scales, const float* zeros, int K, int N,
+                          int group, int gpr) {
+    const size_t ng = (size_t)N * gpr;
+    float* d = static_cast<float*>(device_alloc(2 * ng * sizeof(float)));
+    byhip_q4w* w = nullptr;
+    try {
+        BYHIP_HIP(hipMemcpyAsync(d, scales, ng * 4, hipMemcpyHostToDevice, stream()));
+        BYHIP_HIP(hipMemcpyAsync(d + ng, zeros, ng * 4, hipMemcpyHostToDevice, stream()));
+        w = build_resident_dev(wq_rows, false, d, d + ng, K, N, group, gpr);
+    } catch (...) {
+        device_free(d);
+        throw;
+    }
+    device_free(d);
     return w;
 }
 
@@ -336,14 +359,9 @@ int byhip_q4_resident_from_device(const void* d_wq, size_t wq_off, const void* d
         check_span(static_cast<const uint8_t*>(d_wq) + wq_off, wq_bytes, "Q4 packed weights");
         check_span(d_scales, ng * 4, "Q4 scales");
         check_span(d_zeros, ng * 4, "Q4 zeros");
-        std::vector<uint8_t> wq(wq_bytes);
-        std::vector<float> sc(ng), ze(ng);
-        BYHIP_HIP(hipStreamSynchronize(stream()));
-        BYHIP_HIP(hipMemcpy(wq.data(), static_cast<const uint8_t*>(d_wq) + wq_off, wq_bytes,
-                            hipMemcpyDeviceToHost));
-        BYHIP_HIP(hipMemcpy(sc.data(), d_scales, ng * 4, hipMemcpyDeviceToHost));
-        BYHIP_HIP(hipMemcpy(ze.data(), d_zeros, ng * 4, hipMemcpyDeviceToHost));
-        *out = build_resident(wq.data(), sc.data(), ze.data(), K, N, group_size, groups_per_row);
+        *out = build_resident_dev(static_cast<const uint8_t*>(d_wq) + wq_off, true,
+                                  static_cast<const float*>(d_scales), static_cast<const float*>(d_zeros), K, N,
+                                  group_size, groups_per_row);
     });
 }
 

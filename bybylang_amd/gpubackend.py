@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes as C
 import enum
+import os
 import sys
 from dataclasses import dataclass, field
 
@@ -232,6 +233,59 @@ def residentUploadQ4(backend: GpuBackend, wq, scales, zeros, k: int, n: int, gro
                                           ze.ctypes.data, k, n, groupSize, nGroupsPerRow,
                                           C.byref(h)), "residentUploadQ4")
     return ResidentWeightHandle(gbHip, k, n, groupSize, nGroupsPerRow, wqOffset, h.value)
+
+
+@dataclass
+class MappedReadOnlyFile:
+    """MappedReadOnlyFile, mapped_file.nim:5-8: a read-only mapping of a checkpoint; `data` is the
+    host address of its first byte."""
+    data: int = 0
+    size: int = 0
+    backing: object = None
+
+
+def openReadOnlyMapping(path: str) -> MappedReadOnlyFile:
+    """openReadOnlyMapping, mapped_file.nim:9-13."""
+    import mmap
+    with open(path, "rb") as f:
+        size = os.fstat(f.fileno()).st_size
+        m = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ) if size else None
+    if m is None:
+        return MappedReadOnlyFile(0, 0, None)
+    view = np.frombuffer(m, dtype=np.uint8)
+    return MappedReadOnlyFile(view.ctypes.data, size, (m, view))
+
+
+def unmapReadOnlyFile(mapping: MappedReadOnlyFile) -> None:
+    """unmapReadOnlyFile, mapped_file.nim:15-20."""
+    if mapping.backing is not None:
+        m, view = mapping.backing
+        del view
+        mapping.backing = None
+        m.close()
+    mapping.data = 0
+    mapping.size = 0
+
+
+def residentUploadQ4Mapped(backend: GpuBackend, wq: int, wqBytes: int, scales, zeros, k: int, n: int,
+                           groupSize: int, nGroupsPerRow: int) -> tuple[ResidentWeightHandle, bool]:
+    """residentUploadQ4Mapped, gpubackend.nim:2961-2998: packed weights at host address `wq` (for
+    example inside a MappedReadOnlyFile) are copied straight from the mapping into device memory,
+    never through an intermediate host copy; scales and zeros are small and always copied.
+
+    Returns (weights, zeroCopy). zeroCopy is False: the MI355X keeps weights in its own HBM, and
+    the GPU does not wrap pageable host pages in place here (that would need the pages
+    registered with the runtime), so the copy is the dGPU branch of the reference. The caller may
+    unmap once this returns (the library has its own copy)."""
+    _require_hip(backend)
+    ensureGpuInit(backend)
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    ze = np.ascontiguousarray(zeros, dtype=np.float32)
+    h = C.c_void_p()
+    check(load().byhip_q4_resident_upload(C.c_void_p(wq), wqBytes, 0, sc.ctypes.data, ze.ctypes.data,
+                                          k, n, groupSize, nGroupsPerRow, C.byref(h)),
+          "residentUploadQ4Mapped")
+    return ResidentWeightHandle(gbHip, k, n, groupSize, nGroupsPerRow, 0, h.value), False
 
 
 def residentFreeQ4(w: ResidentWeightHandle) -> None:

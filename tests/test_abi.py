@@ -135,3 +135,23 @@ def test_session_mirror_rejects_other_backends():
     from bybylang_amd import gpubackend as gb
     with pytest.raises(ValueError):
         gb.sessionBegin(gb.gbVulkan)
+
+
+def test_read_only_mapping(tmp_path):
+    """openReadOnlyMapping / unmapReadOnlyFile (mapped_file.nim:9-20): the mapping exposes the
+    file's bytes at `data`; unmapping clears it; an empty file maps to nothing."""
+    import ctypes
+    from bybylang_amd import gpubackend as gb
+    blob = bytes(range(256)) * 17
+    f = tmp_path / "ckpt.bin"
+    f.write_bytes(blob)
+    m = gb.openReadOnlyMapping(str(f))
+    assert m.size == len(blob) and m.data
+    assert ctypes.string_at(m.data, m.size) == blob
+    gb.unmapReadOnlyFile(m)
+    assert m.data == 0 and m.size == 0
+    e = tmp_path / "empty.bin"
+    e.write_bytes(b"")
+    me = gb.openReadOnlyMapping(str(e))
+    assert me.size == 0 and me.data == 0
+    gb.unmapReadOnlyFile(me)

@@ -308,3 +308,36 @@ def test_gpu_matmul_q4_immediate(hip, oracle):
     M, K, N, grp, x, wq, sc, ze, want = golden_q4(5)
     got = gb.gpuMatmulQ4(gb.gbHip, x, wq, sc, ze, M, K, N, grp, K // grp)
     ref_check(got, oracle.matmul_q4(x, wq, sc, ze, M, K, N, grp, K // grp))
+
+
+def test_resident_upload_mapped(hip, tmp_path):
+    """residentUploadQ4Mapped (gpubackend.nim:2961-2998): packed weights inside a mapped checkpoint
+    at an odd offset are copied straight from the mapping; the result matches an upload from an
+    array bit for bit, stays valid after unmapping, and reports no zero-copy (discrete HBM)."""
+    from bybylang_amd import gpubackend as gb
+    from bybylang_amd import synth
+    g = synth.rng(77)
+    K, N, M = 512, 96, 3
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    f = tmp_path / "model.bin"
+    head = b"BYBYCKPT" + bytes(29)  # weights start at byte 37
+    f.write_bytes(head + wq.tobytes() + b"tail")
+    m = gb.openReadOnlyMapping(str(f))
+    wm, zero_copy = gb.residentUploadQ4Mapped(gb.gbHip, m.data + len(head), wq.nbytes, sc, ze, K, N, 32, K // 32)
+    gb.unmapReadOnlyFile(m)
+    assert zero_copy is False
+    wa = gb.residentUploadQ4(gb.gbHip, wq, sc, ze, K, N, 32, K // 32)
+    x = synth.activations(g, M, K, np.float32)
+    assert gb.sessionBegin(gb.gbHip)
+    hx = gb.sessionUpload(gb.gbHip, x.reshape(-1))
+    cm, ca = gb.SessionHandle(), gb.SessionHandle()
+    assert gb.sessionMatmulQ4(gb.gbHip, hx, wm, cm, M)
+    assert gb.sessionMatmulQ4(gb.gbHip, hx, wa, ca, M)
+    assert gb.sessionEnd(gb.gbHip), gb.sessionGetLastError(gb.gbHip)
+    a = gb.sessionRead(gb.gbHip, cm, M * N)
+    b = gb.sessionRead(gb.gbHip, ca, M * N)
+    assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+    for h in (hx, cm, ca):
+        gb.sessionFree(gb.gbHip, h)
+    gb.residentFreeQ4(wm)
+    gb.residentFreeQ4(wa)
