@@ -181,6 +181,23 @@ def bench_c4(dev, synth, steps, warmup):
         flops = sum(2 * M * K * N for _, K, N in C4_OPS)
         out[f"M{M}"] = {"per_op": per_op, "batch_us": per * 1e6,
                         "batch_GBps": layer_bytes[M] / per / 1e9, "batch_TFLOPs": flops / per / 1e12}
+        if M > 1:
+            # residentPrepareQ4 for each projection at this M (plans tuned outside the timed region,
+            # into a fresh plan directory), then the same batch again
+            import tempfile
+            with tempfile.TemporaryDirectory() as d:
+                os.environ["BYHIP_CACHE_DIR"] = d
+                plans = {}
+                for j, (name, K, N) in enumerate(C4_OPS):
+                    for w in weights[j]:
+                        dev.q4_prepare(w, M, dev.F16)
+                    info = dev.q4_plan_info(weights[j][0], M, dev.F16)
+                    plans[name] = info[0] if info else None
+                gpu_s, _ = run_steps(layer, steps, warmup)
+                per = gpu_s / steps
+                out[f"M{M}"]["tuned"] = {"batch_us": per * 1e6, "plans": plans}
+                dev.q4_plans_reset()
+                del os.environ["BYHIP_CACHE_DIR"]
     for ws in weights:
         for w in ws:
             w.close()

@@ -79,6 +79,9 @@ SIGNATURES = {
     "byhip_q4_resident_info": (_I, [_VP, C.POINTER(Q4WInfo)]),
     "byhip_q4_matmul": (_I, [_VP, _I, _VP, _VP, _I, _I]),
     "byhip_q4_matmul_fused": (_I, [_I, _FP, _VP, _I, _VP, _I, _FP, _I, _FP, C.c_float, _I]),
+    "byhip_q4_prepare": (_I, [_VP, _I, _I]),
+    "byhip_q4_plan_info": (_I, [_VP, _I, _I, C.c_char_p, _I, C.POINTER(_I)]),
+    "byhip_q4_plans_reset": (_I, []),
     "byhip_gpu_matmul_q4": (_I, [_FP, _U8P, _FP, _FP, _FP, _I, _I, _I, _I, _I]),
     "byhip_fp4km_tile_gemm": (_I, [_VP, _I, _U8P, _SZ, _SZ, _FP, _SZ, _SZ, _VP, _I, _I, _I, _I]),
     "byhip_mxfp4_gemm": (_I, [_U8P, _U8P, _VP, _I, _I, _I, _I]),

@@ -31,10 +31,23 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+def source_hash() -> str:
+    """FNV-1a (64-bit) of the kernel sources and the C ABI header, in name order: the tuned-plan
+    cache is keyed by it, so plans tuned for other kernels are not reused."""
+    h = 0xCBF29CE484222325
+    files = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.h")) +
+                   glob.glob(os.path.join(INCLUDE, "*.h")))
+    for path in files:
+        with open(path, "rb") as f:
+            for b in os.path.basename(path).encode() + f.read():
+                h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return f"{h:016x}"
+
+
 def common_flags() -> list[str]:
     return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
             "-Wno-unused-function", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            f"-I{INCLUDE}", f"-I{CSRC}"]
+            f"-I{INCLUDE}", f"-I{CSRC}", f'-DBYHIP_SOURCE_HASH="{source_hash()}"']
 
 
 def _compile(src: str) -> str:

@@ -44,6 +44,13 @@ struct GemmArgs {
 // Queues the GEMM on the library stream; K % 32 == 0 is required (callers check).
 void launch_gemm(BFormat fmt, const GemmArgs& a);
 
+// The Q4 GEMM kernels by explicit choice (a tuned plan's candidates): kQ4Pipe, the LDS-staged
+// pipelined kernel with `tile` 1..4 (64x128, 64x64, 32x128, 32x64) and `splits`; kQ4Skinny (M <= 32,
+// `splits`); kQ4General, the general LDS-staged kernel. tile / splits 0 keep the default choice.
+// Returns false, queueing nothing, when that kernel does not take the call.
+enum { kQ4Pipe = 1, kQ4Skinny = 2, kQ4General = 3 };
+bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int splits);
+
 // Native MXFP4 GEMM (E2M1 x E2M1 with E8M0 block scales): x and w in the FP4-KM packing.
 // K % 128 == 0 is required.
 void launch_mxfp4(const uint8_t* x, const uint8_t* x_scales, const uint8_t* w,

@@ -709,9 +709,9 @@ void launch_q4_pipe_shape(const GemmArgs& a, int splits) {
 // split so that the grid holds about two blocks per CU, each split keeping at least `min_steps`
 // steps; the partials must fit the workspace. BYHIP_Q4_SPLIT forces the number of splits. Sets
 // a.part / a.split_steps and returns the number of splits (1: none).
-int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps) {
+int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps, int forced) {
     const long cus = compute_units();
-    long splits = env_int("BYHIP_Q4_SPLIT", 0);
+    long splits = forced > 0 ? forced : env_int("BYHIP_Q4_SPLIT", 0);
     if (splits < 1) splits = tiles >= cus ? 1 : std::min<long>((2 * cus + tiles - 1) / tiles, nsteps / min_steps);
     const long fit = (long)(kWorkspaceBytes / (splitk_stride(a.M, a.N) * sizeof(float)));
     splits = std::max<long>(1, std::min<long>({splits, (long)nsteps, fit}));
@@ -733,14 +733,15 @@ void launch_splitk_sum(const GemmArgs& a, int splits) {
 }
 
 // Tile choice: 64 x 128, or 32 x 128 when M <= 32, split along K when the tiles leave CUs idle.
-// BYHIP_Q4_TILE=1..4 forces 64x128, 64x64, 32x128, 32x64.
-void launch_q4_pipe(const GemmArgs& a0) {
+// BYHIP_Q4_TILE=1..4 forces 64x128, 64x64, 32x128, 32x64; a tuned plan passes tile / splits (0:
+// the default choice).
+void launch_q4_pipe(const GemmArgs& a0, int tile_choice = 0, int split_choice = 0) {
     GemmArgs a = a0;
-    int tile = env_int("BYHIP_Q4_TILE", 0);
+    int tile = tile_choice > 0 ? tile_choice : env_int("BYHIP_Q4_TILE", 0);
     if (tile < 1 || tile > 4) tile = a.M <= 32 ? 3 : 1;
     const int bm = tile <= 2 ? 64 : 32, bn = tile % 2 ? 128 : 64;
     const long tiles = (long)((a.N + bn - 1) / bn) * ((a.M + bm - 1) / bm);
-    const int splits = choose_split(a, tiles, a.K / PBK, 4);
+    const int splits = choose_split(a, tiles, a.K / PBK, 4, split_choice);
     switch (tile) {
     case 1: launch_q4_pipe_shape<64, 128>(a, splits); break;
     case 2: launch_q4_pipe_shape<64, 64>(a, splits); break;
@@ -760,11 +761,11 @@ bool q4_skinny_ok(const GemmArgs& a) {
 }
 
 // Rows per block: 16 or 32 (the smallest that holds M).
-void launch_q4_skinny(const GemmArgs& a0) {
+void launch_q4_skinny(const GemmArgs& a0, int split_choice = 0) {
     GemmArgs a = a0;
     const int bm = a.M <= 16 ? 16 : 32;
     const long tiles = (a.N + kSkinnyCols - 1) / kSkinnyCols;
-    const int splits = choose_split(a, tiles, a.K / 128, 8);
+    const int splits = choose_split(a, tiles, a.K / 128, 8, split_choice);
     if (bm == 16) launch_q4_skinny_shape<16>(a, splits);
     else launch_q4_skinny_shape<32>(a, splits);
     if (a.part) launch_splitk_sum(a, splits);
@@ -794,6 +795,32 @@ void launch_f(const GemmArgs& a) {
 }
 
 }  // namespace
+
+bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int splits) {
+    if (a.K % 32 != 0 || a.M <= 0 || a.N <= 0 || a.M > 65535 * BM) return false;
+    switch (kind) {
+    case kQ4Pipe:
+        if (fmt != BFormat::Q4Fast || !q4_pipe_ok(a)) return false;
+        launch_q4_pipe(a, tile, splits);
+        return true;
+    case kQ4Skinny: {
+        constexpr uint64_t kLim = 0x80000000u;
+        if (fmt != BFormat::Q4Fast || a.K % 128 != 0 || a.M > 32 || !q4_pipe_ok(a) ||
+            (uint64_t)(a.M + 64) * a.K * 2 >= kLim || (uint64_t)(a.N + 64) * a.row_bytes >= kLim ||
+            (uint64_t)(a.N + 64) * a.gpr * 2 >= kLim)
+            return false;
+        launch_q4_skinny(a, splits);
+        return true;
+    }
+    case kQ4General:
+        if (fmt == BFormat::Q4Fast) launch_f<BFormat::Q4Fast>(a);
+        else if (fmt == BFormat::Q4Generic) launch_f<BFormat::Q4Generic>(a);
+        else return false;
+        return true;
+    default:
+        return false;
+    }
+}
 
 void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.K % 32 != 0) fail("byhip: internal: GEMM needs K %% 32 == 0 (K=%d)", a.K);

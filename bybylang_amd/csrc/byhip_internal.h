@@ -46,6 +46,10 @@ int compute_units();
 // stream uses it in stream order.
 constexpr size_t kWorkspaceBytes = 32u << 20;
 void* workspace();
+// Whether a session (or a recording) is open.
+bool session_open();
+// Properties of the initialised device.
+const hipDeviceProp_t& device_props();
 
 // Allocation registry of buffers the library handed out: byte size (0 = not ours) and, for small
 // host uploads, a host copy (decode tables are classified on the host without a device read).

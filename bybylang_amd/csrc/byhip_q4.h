@@ -1,0 +1,29 @@
+// byhip_q4.h - Q4 kernel choice shared by the router and the tuner (internal to libbybyhip.so).
+#pragma once
+
+#include "byhip_internal.h"
+
+namespace byhip {
+
+// A choice of Q4 kernel for one call shape: what byhip_q4_prepare stores and byhip_q4_matmul
+// follows. tile / splits pick the MFMA GEMM's tile (1..4) and split-K (0: the default choice).
+enum Q4PlanKind : int {
+    kPlanGeneric = 1,  // the exact per-element kernel (the tuner's parity baseline)
+    kPlanGemv = 2,     // the decode GEMV
+    kPlanPipe = 3,     // the LDS-staged pipelined MFMA GEMM (benchmark format)
+    kPlanSkinny = 4,   // the skinny MFMA GEMM (M <= 32)
+    kPlanGemm = 5      // the general LDS-staged MFMA GEMM
+};
+struct Q4Plan {
+    int kind = 0;
+    int tile = 0;
+    int splits = 0;
+};
+
+// Queues y = x . W^T with the kernel the plan names; false, queueing nothing, when that kernel
+// does not take this call (the arguments were validated by the caller).
+bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
+// The plan byhip_q4_prepare chose for these weights, this M's class and activation dtype, if any.
+bool q4_lookup_plan(const byhip_q4w* w, int M, int x_dtype, Q4Plan* out);
+
+}  // namespace byhip

@@ -14,6 +14,7 @@
 
 #include "byhip_gemm.h"
 #include "byhip_gemv.h"
+#include "byhip_q4.h"
 #include "byhip_internal.h"
 #include "byhip_kernels.h"
 
@@ -275,6 +276,21 @@ bool zeros_integral(const byhip_q4w* w) {
     return std::floor(z) == z && z >= -1024.0f && z <= 1024.0f;
 }
 
+GemmArgs q4_gemm_args(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
+    GemmArgs a;
+    a.x = x; a.x_dtype = x_dtype; a.y = y; a.y_dtype = y_dtype;
+    a.M = M; a.K = w->K; a.N = w->N;
+    a.wq = w->wq; a.row_bytes = w->row_bytes; a.scales = w->scales; a.scale_f16 = w->scale_f16;
+    a.zeros = w->zeros; a.zero_value = w->zero_value; a.group = w->group; a.gpr = w->gpr;
+    return a;
+}
+
+// Weights the fp16 MFMA kernels take in the Q4Fast form: fp16 scales, an integral uniform zero,
+// group 0 or a multiple of 32.
+bool q4_fast(const byhip_q4w* w) {
+    return w->scale_f16 && zeros_integral(w) && (w->group == 0 || w->group % 32 == 0);
+}
+
 void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
     if (!w) fail("byhip: null Q4 weights");
     if (x_dtype != BYHIP_F32 && x_dtype != BYHIP_F16) fail("byhip: Q4 activations must be F32 or F16");
@@ -284,6 +300,9 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
     check_span(x, (size_t)M * w->K * dtype_bytes(x_dtype), "Q4 activations");
     check_span(y, (size_t)M * w->N * dtype_bytes(y_dtype), "Q4 output");
     const int mode = env_int("BYHIP_Q4_ROUTE", 0);  // 0 auto, 1 GEMV, 2 GEMM, 3 generic
+    // A plan chosen by byhip_q4_prepare for this shape, unless a route is forced.
+    Q4Plan plan;
+    if (mode == 0 && q4_lookup_plan(w, M, x_dtype, &plan) && q4_run_plan(plan, x, x_dtype, w, y, y_dtype, M)) return;
     // The vector kernels read 16-byte words of weights and activations.
     const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (!aligned) {
@@ -306,19 +325,36 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
         launch_generic(x, x_dtype, w, y, y_dtype, M);
         return;
     }
-    GemmArgs a;
-    a.x = x; a.x_dtype = x_dtype; a.y = y; a.y_dtype = y_dtype;
-    a.M = M; a.K = w->K; a.N = w->N;
-    a.wq = w->wq; a.row_bytes = w->row_bytes; a.scales = w->scales; a.scale_f16 = w->scale_f16;
-    a.zeros = w->zeros; a.zero_value = w->zero_value; a.group = w->group; a.gpr = w->gpr;
-    const bool fast = w->scale_f16 && zeros_integral(w) && (w->group == 0 || w->group % 32 == 0);
-    launch_gemm(fast ? BFormat::Q4Fast : BFormat::Q4Generic, a);
+    launch_gemm(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic, q4_gemm_args(x, x_dtype, w, y, y_dtype, M));
 }
 
 }  // namespace
 
 void q4_matmul_run(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
     q4_matmul_impl(x, x_dtype, w, y, y_dtype, M);
+}
+
+bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
+    const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    switch (p.kind) {
+    case kPlanGeneric:
+        launch_generic(x, x_dtype, w, y, y_dtype, M);
+        return true;
+    case kPlanGemv:
+        if (!aligned || M > 8 || !q4_gemv_eligible(w, M, x_dtype)) return false;
+        launch_q4_gemv(x, x_dtype, w, y, y_dtype, M);
+        return true;
+    case kPlanPipe:
+    case kPlanSkinny:
+    case kPlanGemm: {
+        if (!aligned || w->K % 32 != 0) return false;
+        const int kind = p.kind == kPlanPipe ? kQ4Pipe : (p.kind == kPlanSkinny ? kQ4Skinny : kQ4General);
+        return launch_q4_choice(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic,
+                                q4_gemm_args(x, x_dtype, w, y, y_dtype, M), kind, p.tile, p.splits);
+    }
+    default:
+        return false;
+    }
 }
 
 }  // namespace byhip

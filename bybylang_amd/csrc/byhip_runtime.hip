@@ -92,6 +92,8 @@ void enter_compute() {
 hipStream_t stream() { return st().stream; }
 int compute_units() { return st().prop.multiProcessorCount; }
 void* workspace() { return st().workspace; }
+bool session_open() { return st().session_open || st().recording; }
+const hipDeviceProp_t& device_props() { return st().prop; }
 
 void no_host_sync(const char* what) {
     if (st().recording)

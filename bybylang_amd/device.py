@@ -142,6 +142,31 @@ def q4_matmul(x: DeviceBuffer, x_dtype: int, w: Q4Weights, y: DeviceBuffer, y_dt
     check(load().byhip_q4_matmul(x.ptr, x_dtype, w.handle, y.ptr, y_dtype, M), "byhip_q4_matmul")
 
 
+def q4_prepare(w: Q4Weights, M: int, x_dtype: int = F32) -> int:
+    """byhip_q4_prepare: BYHIP_OK when a plan is in place, BYHIP_UNSUPPORTED when tuning is off or
+    a session is open."""
+    rc = load().byhip_q4_prepare(w.handle, M, x_dtype)
+    if rc == _abi.BYHIP_UNSUPPORTED:
+        return rc
+    check(rc, "byhip_q4_prepare")
+    return rc
+
+
+def q4_plan_info(w: Q4Weights, M: int, x_dtype: int = F32):
+    """(plan name, from the plan file) for these weights, or None when there is no plan."""
+    name = C.create_string_buffer(64)
+    cached = C.c_int(0)
+    rc = load().byhip_q4_plan_info(w.handle, M, x_dtype, name, 64, C.byref(cached))
+    if rc == _abi.BYHIP_UNSUPPORTED:
+        return None
+    check(rc, "byhip_q4_plan_info")
+    return name.value.decode(), bool(cached.value)
+
+
+def q4_plans_reset() -> None:
+    check(load().byhip_q4_plans_reset(), "byhip_q4_plans_reset")
+
+
 def q4_matmul_fused(mode: int, a: DeviceBuffer, ws, outs, res: DeviceBuffer = None,
                     gamma: DeviceBuffer = None, eps: float = 0.0) -> int:
     """The fused decode GEMV (byhip_q4_matmul_fused): returns BYHIP_OK, or BYHIP_UNSUPPORTED when

@@ -288,6 +288,19 @@ def residentUploadQ4Mapped(backend: GpuBackend, wq: int, wqBytes: int, scales, z
     return ResidentWeightHandle(gbHip, k, n, groupSize, nGroupsPerRow, 0, h.value), False
 
 
+def residentPrepareQ4(w: ResidentWeightHandle, M: int = 1) -> bool:
+    """residentPrepareQ4, gpubackend.nim:2871-2880: opt-in plan selection for these weights at
+    this M (fp32 activations, the session API's dtype); the ordinary Q4 session calls then use
+    the plan. False when tuning is off or a session is open."""
+    if w.hipWeights is None:
+        return False
+    rc = load().byhip_q4_prepare(w.hipWeights, M, _abi.F32)
+    if rc == _abi.BYHIP_UNSUPPORTED:
+        return False
+    check(rc, "residentPrepareQ4")
+    return True
+
+
 def residentFreeQ4(w: ResidentWeightHandle) -> None:
     """residentFreeQ4, gpubackend.nim:3233-3253."""
     if w.hipWeights:

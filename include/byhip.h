@@ -165,6 +165,24 @@ int byhip_q4_resident_info(const byhip_q4w* w, byhip_q4w_info* out);
  * BYHIP_F16 or BYHIP_BF16. M <= 8 runs the decode GEMV, larger M the MFMA GEMM. */
 int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
 
+/* residentPrepareQ4 (gpubackend.nim:2871-2880; vulkanPrepareQ4Tuned, q4_autotune.nim:387-543):
+ * chooses the kernel byhip_q4_matmul uses for these weights, this M's class (1; 2..32; 33..128;
+ * more, tuned at M = 1, 32, 64 and 256) and activation dtype (BYHIP_F32 is the reference's session
+ * dtype).
+ * Every candidate runs once on deterministic input and must match the exact per-element kernel
+ * within 1e-4 of the output's magnitude (3e-3 for kernels that round weights to fp16 for the MFMA)
+ * with finite outputs; the survivors are timed and the fastest by at least 3% is kept, in memory
+ * and in a plan file under BYHIP_CACHE_DIR (else $XDG_CACHE_HOME/bybylang_amd or
+ * ~/.cache/bybylang_amd) keyed by the device and the library's kernel sources, so a later process
+ * reuses it (q4_autotune.nim:32-50). Returns BYHIP_UNSUPPORTED when tuning is off
+ * (BYHIP_Q4_TUNED=0 or BYHIP_GPU_AUTOTUNE=0) or a session is open, as the reference does. */
+int byhip_q4_prepare(const byhip_q4w* w, int M, int x_dtype);
+/* The plan in place for these weights, M class and dtype: its name and whether it came from the
+ * plan file (1) or was tuned in this process (0); BYHIP_UNSUPPORTED when there is none. */
+int byhip_q4_plan_info(const byhip_q4w* w, int M, int x_dtype, char* name, int name_len, int* from_cache);
+/* Forgets this process's plans (the plan file stays; the next prepare reads it again). */
+int byhip_q4_plans_reset(void);
+
 /* sessionMatmulQ4Fused (gpubackend.nim:3185-3231; its shader, q4_autotune.nim:194-330): the fused
  * decode GEMV, M = 1, on fp32 device buffers.
  *   mode 0: ws[0..n_ws-1] (1..3 resident weights of equal K, group and groups per row) share `a`
