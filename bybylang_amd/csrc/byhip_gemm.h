@@ -46,9 +46,10 @@ void launch_gemm(BFormat fmt, const GemmArgs& a);
 
 // The Q4 GEMM kernels by explicit choice (a tuned plan's candidates): kQ4Pipe, the LDS-staged
 // pipelined kernel with `tile` 1..4 (64x128, 64x64, 32x128, 32x64) and `splits`; kQ4Skinny (M <= 32,
-// `splits`); kQ4General, the general LDS-staged kernel. tile / splits 0 keep the default choice.
+// `splits`); kQ4General, the general LDS-staged kernel; kQ4Big, the 128 x 256 prefill tile, and
+// kQ4Wide, the 64 x 128 skinny tile (`splits`). tile / splits 0 keep the default choice.
 // Returns false, queueing nothing, when that kernel does not take the call.
-enum { kQ4Pipe = 1, kQ4Skinny = 2, kQ4General = 3 };
+enum { kQ4Pipe = 1, kQ4Skinny = 2, kQ4General = 3, kQ4Big = 4, kQ4Wide = 5 };
 bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int splits);
 
 // Native MXFP4 GEMM (E2M1 x E2M1 with E8M0 block scales): x and w in the FP4-KM packing.

@@ -479,7 +479,7 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 // Skinny Q4 GEMM for small M (the decode-batch and short-prefill shapes): weights are read once,
 // straight from HBM into MFMA operand registers, so the kernel streams them like the GEMV while the
 // MFMAs do the row products. Same format conditions as q4_gemm_pipe, K % 128 == 0, M <= 32.
-//   Block: 4 waves on the same kSkinnyCols columns (fragments of 16) and BM rows (BM / 16
+//   Block: 4 waves on the same 16 FN columns (FN fragments of 16) and BM rows (BM / 16
 //   fragments);
 //   the block's K steps of 128 are dealt round-robin to its waves, and the four partial tiles are
 //   added through LDS at the end (wave order 0 + 1 + 2 + 3).
@@ -493,34 +493,37 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 //   16-byte chunk c of row r at slot c ^ (r & 15): the fragment reads (16 rows, one chunk each)
 //   then hit 16 distinct bank groups. Each wave reads only what it loaded, so no barrier is
 //   needed; the double buffer and a vmcnt wait order the direct loads and the reads.
-constexpr int kSkinnyFN = 4;                 // column fragments per block (and per wave)
-constexpr int kSkinnyCols = 16 * kSkinnyFN;  // columns per block
-
-template <int BM>
+//   Shapes: BM x 16 FN with FN = 4 column fragments for BM <= 32 (two blocks per CU), and the
+//   wide tile BM = 64, FN = 8 for prefill (one block per CU, 128 accumulators per lane): there
+//   each dequantized weight fragment feeds four row fragments and each activation fragment eight
+//   column fragments, so the dequantization VALU work and the LDS reads per MFMA both halve.
+template <int FN>
 struct SkinnyW {
-    v4u w[kSkinnyFN];       // 32 nibbles of one column per fragment
-    uint32_t s[kSkinnyFN];  // their fp16 scale
+    v4u w[FN];       // 32 nibbles of one column per fragment
+    uint32_t s[FN];  // their fp16 scale
 };
 
-template <int BM>
+template <int BM, int FN>
 struct SkinnyLds {
     static constexpr int kX = 4 * 2 * BM * 256;               // 4 waves x 2 buffers x BM rows x 256 bytes
-    static constexpr int kRed = 4 * (BM / 16) * kSkinnyFN * 4 * 64 * 4;  // 4 partial tiles of the block
+    static constexpr int kRed = 4 * (BM / 16) * FN * 4 * 64 * 4;  // 4 partial tiles of the block
     static constexpr int kBytes = kX > kRed ? kX : kRed;
 };
 
-template <int BM, int YT>
-__global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
-    constexpr int FM = BM / 16, FN = kSkinnyFN, NV = FM * FN * 4;  // accumulator floats per lane
+constexpr int skinny_waves_per_simd(int BM, int FN) { return BM * FN > 128 ? 1 : 2; }
+
+template <int BM, int FN, int YT>
+__global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_skinny(GemmArgs a) {
+    constexpr int FM = BM / 16, NV = FM * FN * 4;  // accumulator floats per lane
     constexpr int XDMA = BM / 4;                           // direct loads per step (4 rows each)
     constexpr int XBUF = BM * 256;                         // bytes of one activation buffer
-    __shared__ __attribute__((aligned(16))) uint8_t lds[SkinnyLds<BM>::kBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[SkinnyLds<BM, FN>::kBytes];
 
     // wid is wave-uniform; readfirstlane tells the compiler so, which keeps the step logic in
     // scalar registers and branches.
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * kSkinnyCols, m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * (16 * FN), m0 = blockIdx.y * BM;
     const int K = a.K;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
     const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
@@ -532,25 +535,27 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     const rsrc_t sr = make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
     const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
     // Direct load u of a step: lane -> row 4u + lane / 16, LDS slot lane % 16 holding chunk
-    // slot ^ (row & 15) of that row.
-    uint32_t xo[XDMA];
+    // slot ^ (row & 15) of that row. Loads u and u + 4 differ by 16 rows and share the slot
+    // pattern, so four lane offsets serve them all; the rest of every offset is wave-uniform and
+    // travels in the scalar offset, as does each column fragment's row of weights and scales.
+    uint32_t xo[4];
 #pragma unroll
-    for (int u = 0; u < XDMA; ++u) {
-        const int r = 4 * u + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
-        xo[u] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
+    for (int q = 0; q < 4; ++q) {
+        const int r = 4 * q + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+        xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
-    uint32_t wo[FN], so[FN];
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        wo[j] = (uint32_t)(n0 + 16 * j + c) * (uint32_t)a.row_bytes + 16u * g;
-        so[j] = (uint32_t)(n0 + 16 * j + c) * (uint32_t)a.gpr;
-    }
+    const uint32_t xrow16 = 16u * (uint32_t)K * 2u;  // 16 activation rows
+    const uint32_t wo = (uint32_t)(n0 + c) * (uint32_t)a.row_bytes + 16u * g;
+    const uint32_t so = (uint32_t)(n0 + c) * (uint32_t)a.gpr;
+    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes, sfrag = 32u * (uint32_t)a.gpr;  // per fragment
     uint8_t* const xbuf = lds + wid * 2 * XBUF;
 
-    // Step t of this wave is block step (wid + 4t + rot) mod nsteps. The rotation by the block
-    // index staggers where blocks start along K.
+    // Step t of this wave is block step (wid + 4t + rot) mod nsteps. For the narrow tiles the
+    // rotation by the block index staggers where blocks start along K; the wide tile keeps every
+    // block on the same K slice at about the same time, so the column blocks that share an
+    // activation slice find it in L2 (measured faster at prefill shapes).
     const int nt = nsteps > wid ? (nsteps - wid + 3) / 4 : 0;
-    const int rot = nsteps > 0 ? (int)(blockIdx.x % (unsigned)nsteps) : 0;
+    const int rot = nsteps > 0 && FN <= 4 ? (int)(blockIdx.x % (unsigned)nsteps) : 0;
     auto kstep = [&](int t) {
         const int v = wid + 4 * t + rot;
         return v >= nsteps ? v - nsteps : v;
@@ -559,18 +564,20 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     // loads. A step past the wave's last one (t >= nt) adds 2^31 through the scalar offset, which
     // every resource rejects: it reads zeros without touching memory, so the loads need no branch
     // around them and every step leaves the same number in flight.
-    auto load = [&](SkinnyW<BM>& r, uint8_t* __restrict__ dst, int t) {
+    auto load = [&](SkinnyW<FN>& r, uint8_t* __restrict__ dst, int t) {
         const bool ok = t < nt;
         const uint32_t k0 = (uint32_t)(s_first + (ok ? kstep(t) : 0)) * 128u;
         const uint32_t oob = ok ? 0u : 0x80000000u;
         const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
 #pragma unroll
         for (int u = 0; u < XDMA; ++u)
-            lds_dma16(xr, dst + 1024 * u, xo[u] + 2u * k0, oob);
+            lds_dma16(xr, dst + 1024 * u, xo[u & 3] + 2u * k0, oob + (uint32_t)(u >> 2) * xrow16);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo[j] + (k0 >> 1), oob, 2);
+        for (int j = 0; j < FN; ++j)
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 2);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (so[j] + grp), oob, 0);
+        for (int j = 0; j < FN; ++j)
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (so + grp), oob + (uint32_t)j * sfrag, 0);
     };
 
     const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
@@ -585,29 +592,34 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const SkinnyW<BM>& r, const uint8_t* __restrict__ src) {
+    auto compute = [&](const SkinnyW<FN>& r, const uint8_t* __restrict__ src) {
         h2 ss[FN];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const _Float16 sc = bits_h((uint16_t)r.s[j]);
             ss[j] = (h2){sc, sc};
         }
-        uint4 xv[4][FM];  // the step's activation fragments, all read before the math
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
+        // The step's activation fragments, read ahead of the math: all four MFMA columns (kk) up
+        // front when the block is narrow, two columns ahead when the wide tile needs the registers.
+        constexpr int XA = FN > 4 ? 2 : 4;
+        uint4 xv[XA][FM];
+        auto xread = [&](int kk) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                xv[kk][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
+                xv[kk % XA][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
+        };
+#pragma unroll
+        for (int kk = 0; kk < XA; ++kk) xread(kk);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             h8 bw[FN], ax[FM];
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                const uint4 u = perm8(xv[kk][i]);
+                const uint4 u = perm8(xv[kk % XA][i]);
                 ax[i] = *reinterpret_cast<const h8*>(&u);
             }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
+            if (kk + XA < 4) xread(kk + XA);
+            auto dequant = [&](int j) {
                 const uint32_t d = r.w[j][kk], d8 = d >> 8;
                 const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
                 const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
@@ -616,12 +628,25 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
                 const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss[j]), h2_bits((q1 - zz_hi) * ss[j]),
                                            h2_bits((q2 - zz_lo) * ss[j]), h2_bits((q3 - zz_hi) * ss[j]));
                 bw[j] = *reinterpret_cast<const h8*>(&u);
+            };
+            if constexpr (FN > 4) {
+                // wide tile: each weight fragment is dequantized just before its four MFMAs
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    dequant(j);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) dequant(j);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
         }
     };
 
@@ -630,9 +655,9 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     // order; the wait leaves exactly the next step's loads in flight, so this step's activations
     // have landed in LDS (the compiler cannot see that dependence) and its weights and scales are
     // in registers.
-    SkinnyW<BM> ra, rb;
+    SkinnyW<FN> ra, rb;
     load(ra, xbuf, 0);
-    auto step = [&](int t, const SkinnyW<BM>& cur, SkinnyW<BM>& nxt, const uint8_t* __restrict__ xcur,
+    auto step = [&](int t, const SkinnyW<FN>& cur, SkinnyW<FN>& nxt, const uint8_t* __restrict__ xcur,
                     uint8_t* __restrict__ xnxt) {
         __builtin_amdgcn_sched_barrier(0);
         load(nxt, xnxt, t + 1);
@@ -641,10 +666,19 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
         compute(cur, xcur);
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (int t = 0; t < nt; t += 2) {
-        step(t, ra, rb, xbuf, xbuf + XBUF);
-        if (t + 1 >= nt) break;
-        step(t + 1, rb, ra, xbuf + XBUF, xbuf);
+    if constexpr (FN > 4) {
+        // One step per iteration, the next step's registers copied over: with 128 accumulators the
+        // register allocator keeps them in place only in a single-step loop body.
+        for (int t = 0; t < nt; t += 2) {
+            step(t, ra, rb, xbuf, xbuf + XBUF);
+            step(t + 1, rb, ra, xbuf + XBUF, xbuf);
+        }
+    } else {
+        for (int t = 0; t < nt; t += 2) {
+            step(t, ra, rb, xbuf, xbuf + XBUF);
+            if (t + 1 >= nt) break;
+            step(t + 1, rb, ra, xbuf + XBUF, xbuf);
+        }
     }
 
     // Partial tiles of the four waves -> LDS (over the activation buffers, once every wave is done
@@ -673,6 +707,189 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     }
 }
 
+// Large-tile Q4 GEMM for prefill: a 128 x 256 tile per block, so each activation byte is read once
+// per 256 columns and each weight byte once per 128 rows. Every operand byte reaches the CU through
+// its vector L1, whose miss handling (outstanding line fills times L2 latency) is what bounds the
+// smaller tiles at these shapes; the larger tile needs about half the bytes per output.
+//   Block: 4 waves; wave w owns columns 64w .. 64w+63 of the tile and all 128 rows (8 x 4
+//   fragments, 128 accumulators), and the block shares the activation tile.
+//   K steps of 128: in MFMA kk (0..3) lane group g supplies values 32g + 8kk .. 32g + 8kk + 7 in
+//   natural order; a lane's weights for a step are one 16-byte load of one 32-value group, and its
+//   scale.
+//   Activations: the step's 128 x 128 slice moves straight from global memory into LDS with direct
+//   loads (wave w the rows 32w .. 32w+31, 16 lanes per row), chunk c of row r at slot c ^ (r & 15)
+//   as in the skinny kernel. Three LDS buffers and three weight register sets keep the loads of the
+//   next two steps in flight while a step computes. One barrier per step, after each wave's wait
+//   for its own loads of the step, makes every wave's direct loads visible and tells the block that
+//   the buffer the next loads overwrite (read two steps earlier) is free.
+//   Split-K: block z covers the K steps [z * split_steps, ...) and writes fp32 partials.
+constexpr int kBigM = 128, kBigN = 256;
+constexpr int kBigBuf = kBigM * 256;            // bytes of one activation buffer
+constexpr int kBigFM = kBigM / 16, kBigFN = 4;  // fragments per wave
+constexpr int kBigLoads = kBigM / 16 + 2 * kBigFN;  // vector memory instructions per wave and step
+
+struct BigW {
+    v4u w[kBigFN];       // 32 nibbles of one column per fragment
+    uint32_t s[kBigFN];  // their fp16 scale
+};
+
+// Waits for this wave's loads except the newest N, then the workgroup barrier; the memory clobber
+// keeps LDS accesses on their side of it, and the direct loads issued last stay in flight.
+template <int N>
+__device__ __forceinline__ void lds_step_barrier() {
+    wait_vmcnt<N>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int YT>
+__global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kBigBuf];
+
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * kBigN, m0 = blockIdx.y * kBigM;
+    const int K = a.K;
+    const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
+    const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
+
+    // Rows past M and columns past N read zeros through the range checks (the launcher keeps every
+    // offset, with the rows and columns the tile reaches past M and N, below 2^31).
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
+    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
+    const rsrc_t sr = make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
+    const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
+
+    // Direct load u (0..7) of wave w: lane -> row 32w + 4u + lane / 16, LDS slot lane % 16 holding
+    // chunk slot ^ (row & 15). Loads u and u + 4 share the slot pattern; the rest of each offset is
+    // wave-uniform and goes in the scalar offset, as does each column fragment's row.
+    uint32_t xo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 32 * wid + 4 * q + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+        xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
+    }
+    const uint32_t xrow16 = 16u * (uint32_t)K * 2u;
+    const int ncol = n0 + 64 * wid + c;
+    const uint32_t wo = (uint32_t)ncol * (uint32_t)a.row_bytes + 16u * g;
+    const uint32_t so = (uint32_t)ncol * (uint32_t)a.gpr;
+    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes, sfrag = 32u * (uint32_t)a.gpr;
+    uint8_t* const xdst = lds + 32 * 256 * wid;  // this wave's rows of each buffer
+
+    // A step past the block's last one adds 2^31 through the scalar offset: every resource rejects
+    // it, so it reads zeros without touching memory and every step issues the same loads.
+    auto load = [&](BigW& r, int buf, int t) {
+        const bool ok = t < nsteps;
+        const uint32_t k0 = (uint32_t)(s_first + (ok ? t : 0)) * 128u;
+        const uint32_t oob = ok ? 0u : 0x80000000u;
+        const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
+        uint8_t* const dst = xdst + buf * kBigBuf;
+#pragma unroll
+        for (int u = 0; u < kBigM / 16; ++u)
+            lds_dma16(xr, dst + 1024 * u, xo[u & 3] + 2u * k0, oob + (uint32_t)(u >> 2) * xrow16);
+#pragma unroll
+        for (int j = 0; j < kBigFN; ++j)
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 2);
+#pragma unroll
+        for (int j = 0; j < kBigFN; ++j)
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (so + grp), oob + (uint32_t)j * sfrag, 0);
+    };
+
+    // Natural-order dequantization: v_perm_b32 copies byte b of the word (values 2b, 2b + 1) to
+    // bytes 0 and 2, the AND-OR keeps the low nibble in the low half and the high nibble in bits
+    // 4-7 of the high half against the exponent word 0x5400 6400: (1024 + q[2b], 64 + q[2b + 1]),
+    // both exact. The activations then need no permutation.
+    const h2 zz = {(_Float16)(1024.0f + a.zero_value), (_Float16)(64.0f + a.zero_value)};
+    uint32_t mag;
+    asm volatile("v_mov_b32 %0, 0x54006400" : "=v"(mag));
+
+    f4 acc[kBigFM][kBigFN];
+#pragma unroll
+    for (int i = 0; i < kBigFM; ++i)
+#pragma unroll
+        for (int j = 0; j < kBigFN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const BigW& r, int buf) {
+        const uint8_t* const src = lds + buf * kBigBuf;
+        h2 ss[kBigFN];
+#pragma unroll
+        for (int j = 0; j < kBigFN; ++j) {
+            const _Float16 sc = bits_h((uint16_t)r.s[j]);
+            ss[j] = (h2){sc, sc};
+        }
+        // the activation fragments of MFMA column kk, read one column ahead of the math
+        uint4 xv[2][kBigFM];
+        auto xread = [&](int kk) {
+#pragma unroll
+            for (int i = 0; i < kBigFM; ++i)
+                xv[kk & 1][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
+        };
+        xread(0);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            h8 ax[kBigFM];
+#pragma unroll
+            for (int i = 0; i < kBigFM; ++i) ax[i] = *reinterpret_cast<const h8*>(&xv[kk & 1][i]);
+            if (kk < 3) xread(kk + 1);
+#pragma unroll
+            for (int j = 0; j < kBigFN; ++j) {
+                const uint32_t d = r.w[j][kk];
+                uint32_t q[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t rep = __builtin_amdgcn_perm(d, d, 0x01010101u * (uint32_t)b);
+                    q[b] = h2_bits((bits_h2((rep & 0x00F0000Fu) | mag) - zz) * ss[j]);
+                }
+                const uint4 u = make_uint4(q[0], q[1], q[2], q[3]);
+                const h8 bw = *reinterpret_cast<const h8*>(&u);
+#pragma unroll
+                for (int i = 0; i < kBigFM; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw, acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    // Step t: its loads have landed once only the next step's remain; the barrier; the loads of
+    // step t + 2 into the buffer step t - 1 used; the math.
+    BigW r0, r1, r2;
+    load(r0, 0, 0);
+    load(r1, 1, 1);
+    auto step = [&](int t, const BigW& cur, int cbuf, BigW& nxt2, int nbuf) {
+        __builtin_amdgcn_sched_barrier(0);
+        lds_step_barrier<kBigLoads>();
+        __builtin_amdgcn_sched_barrier(0);
+        load(nxt2, nbuf, t + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(cur, cbuf);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int t = 0;
+    for (; t + 3 <= nsteps; t += 3) {
+        step(t, r0, 0, r2, 2);
+        step(t + 1, r1, 1, r0, 0);
+        step(t + 2, r2, 2, r1, 1);
+    }
+    if (t < nsteps) step(t, r0, 0, r2, 2);
+    if (t + 1 < nsteps) step(t + 1, r1, 1, r0, 0);
+    wait_vmcnt<0>();
+
+    // Accumulator (i, j, r) of lane l: row 16i + 4(l / 16) + r, column 64w + 16j + l % 16.
+    float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
+#pragma unroll
+    for (int i = 0; i < kBigFM; ++i)
+#pragma unroll
+        for (int j = 0; j < kBigFN; ++j) {
+            const int n = n0 + 64 * wid + 16 * j + c;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 16 * i + 4 * g + r;
+                if (m < a.M && n < a.N) {
+                    if (part) part[(size_t)m * a.N + n] = acc[i][j][r];
+                    else store_y<YT>(a.y, (size_t)m * a.N + n, acc[i][j][r]);
+                }
+            }
+        }
+}
+
 // Whether the pipelined Q4 kernel takes these arguments.
 bool q4_pipe_ok(const GemmArgs& a) {
     const bool pow2_group = a.group % 32 == 0 && ((a.group >> 5) & ((a.group >> 5) - 1)) == 0;
@@ -683,13 +900,13 @@ bool q4_pipe_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 128) * a.gpr * 2 < kOutOfRange;
 }
 
-template <int BM>
+template <int BM, int FN>
 void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
-    const dim3 grid((a.N + kSkinnyCols - 1) / kSkinnyCols, (a.M + BM - 1) / BM, splits);
+    const dim3 grid((a.N + 16 * FN - 1) / (16 * FN), (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((q4_gemm_skinny<BM, BYHIP_BF16>), grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_skinny<BM, FN, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_skinny<BM, FN, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
+    default: hipLaunchKernelGGL((q4_gemm_skinny<BM, FN, BYHIP_BF16>), grid, dim3(256), 0, stream(), a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_skinny");
 }
@@ -706,13 +923,14 @@ void launch_q4_pipe_shape(const GemmArgs& a, int splits) {
 }
 
 // Split-K for a grid of `tiles` blocks over `nsteps` K steps: when the tiles leave CUs idle, K is
-// split so that the grid holds about two blocks per CU, each split keeping at least `min_steps`
-// steps; the partials must fit the workspace. BYHIP_Q4_SPLIT forces the number of splits. Sets
-// a.part / a.split_steps and returns the number of splits (1: none).
-int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps, int forced) {
+// split so that the grid holds about `per_cu` blocks per CU, each split keeping at least
+// `min_steps` steps; the partials must fit the workspace. BYHIP_Q4_SPLIT forces the number of
+// splits. Sets a.part / a.split_steps and returns the number of splits (1: none).
+int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps, int forced, int per_cu = 2) {
     const long cus = compute_units();
     long splits = forced > 0 ? forced : env_int("BYHIP_Q4_SPLIT", 0);
-    if (splits < 1) splits = tiles >= cus ? 1 : std::min<long>((2 * cus + tiles - 1) / tiles, nsteps / min_steps);
+    if (splits < 1)
+        splits = tiles >= cus ? 1 : std::min<long>((per_cu * cus + tiles - 1) / tiles, nsteps / min_steps);
     const long fit = (long)(kWorkspaceBytes / (splitk_stride(a.M, a.N) * sizeof(float)));
     splits = std::max<long>(1, std::min<long>({splits, (long)nsteps, fit}));
     if (splits == 1) return 1;
@@ -760,15 +978,92 @@ bool q4_skinny_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 64) * a.gpr * 2 < kLim;
 }
 
-// Rows per block: 16 or 32 (the smallest that holds M).
-void launch_q4_skinny(const GemmArgs& a0, int split_choice = 0) {
+// Whether the wide tile (64 x 128) takes the call: the pipelined kernel's conditions, K % 128 == 0
+// and all operand offsets, including the rows and columns a tile reaches past M and N, below 2^31.
+bool q4_wide_ok(const GemmArgs& a) {
+    constexpr uint64_t kLim = 0x80000000u;
+    return a.K % 128 == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + 64) * a.K * 2 < kLim &&
+           (uint64_t)(a.N + 128) * a.row_bytes < kLim && (uint64_t)(a.N + 128) * a.gpr * 2 < kLim;
+}
+
+// Whether the large-tile kernel takes the call: the pipelined kernel's conditions, K % 128 == 0 and
+// all operand offsets, with the rows and columns a tile reaches past M and N, below 2^31.
+bool q4_big_ok(const GemmArgs& a) {
+    constexpr uint64_t kLim = 0x80000000u;
+    return a.K % 128 == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + kBigM) * a.K * 2 < kLim &&
+           (uint64_t)(a.N + kBigN) * a.row_bytes < kLim && (uint64_t)(a.N + kBigN) * a.gpr * 2 < kLim;
+}
+
+int q4_big_splits(const GemmArgs& a);
+
+// The large tile with one block per CU, K split as q4_big_splits says (or `split_choice`).
+void launch_q4_big(const GemmArgs& a0, int split_choice = 0) {
     GemmArgs a = a0;
-    const int bm = a.M <= 16 ? 16 : 32;
-    const long tiles = (a.N + kSkinnyCols - 1) / kSkinnyCols;
-    const int splits = choose_split(a, tiles, a.K / 128, 8, split_choice);
-    if (bm == 16) launch_q4_skinny_shape<16>(a, splits);
-    else launch_q4_skinny_shape<32>(a, splits);
+    const long tiles = (long)((a.N + kBigN - 1) / kBigN) * ((a.M + kBigM - 1) / kBigM);
+    const int nsteps = a.K / 128;
+    const int splits = choose_split(a, tiles, nsteps, 4, split_choice > 0 ? split_choice : q4_big_splits(a));
+    const dim3 grid((a.N + kBigN - 1) / kBigN, (a.M + kBigM - 1) / kBigM, splits);
+    switch (a.y_dtype) {
+    case BYHIP_F32: hipLaunchKernelGGL(q4_gemm_big<BYHIP_F32>, grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL(q4_gemm_big<BYHIP_F16>, grid, dim3(256), 0, stream(), a); break;
+    default: hipLaunchKernelGGL(q4_gemm_big<BYHIP_BF16>, grid, dim3(256), 0, stream(), a); break;
+    }
+    BYHIP_LAUNCHED("q4_gemm_big");
     if (a.part) launch_splitk_sum(a, splits);
+}
+
+// Rows per block: 16 or 32 (the smallest that holds M) with 64 columns and two blocks per CU, or
+// the wide 64 x 128 tile with one block per CU.
+void launch_q4_skinny(const GemmArgs& a0, int split_choice = 0, bool wide = false) {
+    GemmArgs a = a0;
+    const int bm = wide ? 64 : a.M <= 16 ? 16 : 32, cols = wide ? 128 : 64;
+    const long tiles = (long)((a.N + cols - 1) / cols) * ((a.M + bm - 1) / bm);
+    const int splits = choose_split(a, tiles, a.K / 128, 8, split_choice, wide ? 1 : 2);
+    if (wide) launch_q4_skinny_shape<64, 8>(a, splits);
+    else if (bm == 16) launch_q4_skinny_shape<16, 4>(a, splits);
+    else launch_q4_skinny_shape<32, 4>(a, splits);
+    if (a.part) launch_splitk_sum(a, splits);
+}
+
+// Splits launch_q4_big chooses: K is split when the tiles fill at most half the CUs, into as many
+// slices as keep the grid within one block per CU (each slice at least 4 steps).
+int q4_big_splits(const GemmArgs& a) {
+    const long tiles = (long)((a.N + kBigN - 1) / kBigN) * ((a.M + kBigM - 1) / kBigM);
+    const int forced = env_int("BYHIP_Q4_SPLIT", 0);
+    if (forced > 0) return forced;
+    return (int)std::max<long>(1, std::min<long>(compute_units() / tiles, a.K / 128 / 4));
+}
+
+// The Q4 prefill kernel (M above the skinny kernel's range) for the benchmark format, from
+// measurements on MI355X:
+//   the 64 x 128 wide skinny tile when its tiles alone fill the CUs while 128 x 256 tiles would
+//   leave more than half of them idle (M = 512, N = K = 4096: 34 us against 38 us);
+//   else, for M > 64, the 128 x 256 tile, which reads about half the operand bytes per output,
+//   unless the split-K it needs to fill the CUs would move more partial-sum bytes (8 per output
+//   and split: written, then read) than its tiles read operand bytes (400 per tile and K value);
+//   it wins on M = 256 gate+up (82 us against 130 us) and on the K = 14336 down projection, and
+//   loses with 8 splits of K = 4096 (M = 128 or 256, N = 4096), where the wide tile is used, as
+//   it is for M <= 64 (half-empty large tiles);
+//   the pipelined kernel where neither takes the call (K % 128 != 0, offsets past 2^31).
+// BYHIP_Q4_PREFILL forces one: 1 the pipelined kernel, 2 the large tile, 3 the wide skinny tile,
+// when it takes the call. Returns kQ4Pipe / kQ4Big / kQ4Wide, or 0 for the general kernel.
+int q4_prefill_kind(const GemmArgs& a) {
+    const int forced = env_int("BYHIP_Q4_PREFILL", 0);
+    const bool big = q4_big_ok(a), wide = q4_wide_ok(a), pipe = q4_pipe_ok(a);
+    if (forced == 1) return pipe ? kQ4Pipe : 0;
+    if (forced == 2 && big) return kQ4Big;
+    if (forced == 3 && wide) return kQ4Wide;
+    const long cus = compute_units();
+    const long big_tiles = (long)((a.N + kBigN - 1) / kBigN) * ((a.M + kBigM - 1) / kBigM);
+    const long wide_tiles = (long)((a.N + 127) / 128) * ((a.M + 63) / 64);
+    if (wide && wide_tiles >= cus && 2 * big_tiles < cus) return kQ4Wide;
+    if (big && (a.M > 64 || !wide)) {
+        const double splits = q4_big_splits(a);
+        const double partial = splits > 1 ? 8.0 * a.M * a.N * splits : 0.0;
+        if (!wide || partial <= 400.0 * big_tiles * a.K) return kQ4Big;
+    }
+    if (wide) return kQ4Wide;
+    return pipe ? kQ4Pipe : 0;
 }
 
 template <BFormat F, bool XF32>
@@ -812,6 +1107,14 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
         launch_q4_skinny(a, splits);
         return true;
     }
+    case kQ4Big:
+        if (fmt != BFormat::Q4Fast || !q4_big_ok(a)) return false;
+        launch_q4_big(a, splits);
+        return true;
+    case kQ4Wide:
+        if (fmt != BFormat::Q4Fast || !q4_wide_ok(a)) return false;
+        launch_q4_skinny(a, splits, true);
+        return true;
     case kQ4General:
         if (fmt == BFormat::Q4Fast) launch_f<BFormat::Q4Fast>(a);
         else if (fmt == BFormat::Q4Generic) launch_f<BFormat::Q4Generic>(a);
@@ -828,9 +1131,16 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.M > 65535 * BM) fail("byhip: M=%d too large for one launch", a.M);
     switch (fmt) {
     case BFormat::Q4Fast:
-        if (q4_skinny_ok(a)) launch_q4_skinny(a);
-        else if (q4_pipe_ok(a)) launch_q4_pipe(a);
-        else launch_f<BFormat::Q4Fast>(a);
+        if (q4_skinny_ok(a)) {
+            launch_q4_skinny(a);
+            break;
+        }
+        switch (q4_prefill_kind(a)) {
+        case kQ4Big: launch_q4_big(a); break;
+        case kQ4Wide: launch_q4_skinny(a, 0, true); break;
+        case kQ4Pipe: launch_q4_pipe(a); break;
+        default: launch_f<BFormat::Q4Fast>(a); break;
+        }
         break;
     case BFormat::Q4Generic: launch_f<BFormat::Q4Generic>(a); break;
     case BFormat::Fp4Km: launch_f<BFormat::Fp4Km>(a); break;

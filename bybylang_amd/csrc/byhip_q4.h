@@ -12,7 +12,10 @@ enum Q4PlanKind : int {
     kPlanGemv = 2,     // the decode GEMV
     kPlanPipe = 3,     // the LDS-staged pipelined MFMA GEMM (benchmark format)
     kPlanSkinny = 4,   // the skinny MFMA GEMM (M <= 32)
-    kPlanGemm = 5      // the general LDS-staged MFMA GEMM
+    kPlanGemm = 5,     // the general LDS-staged MFMA GEMM
+    kPlanBig = 6,      // the 128 x 256 prefill tile
+    kPlanWide = 7,     // the 64 x 128 skinny prefill tile
+    kPlanLast = kPlanWide
 };
 struct Q4Plan {
     int kind = 0;

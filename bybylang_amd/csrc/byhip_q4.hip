@@ -346,9 +346,15 @@ bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w
         return true;
     case kPlanPipe:
     case kPlanSkinny:
-    case kPlanGemm: {
+    case kPlanGemm:
+    case kPlanBig:
+    case kPlanWide: {
         if (!aligned || w->K % 32 != 0) return false;
-        const int kind = p.kind == kPlanPipe ? kQ4Pipe : (p.kind == kPlanSkinny ? kQ4Skinny : kQ4General);
+        const int kind = p.kind == kPlanPipe     ? kQ4Pipe
+                         : p.kind == kPlanSkinny ? kQ4Skinny
+                         : p.kind == kPlanBig    ? kQ4Big
+                         : p.kind == kPlanWide   ? kQ4Wide
+                                                 : kQ4General;
         return launch_q4_choice(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic,
                                 q4_gemm_args(x, x_dtype, w, y, y_dtype, M), kind, p.tile, p.splits);
     }

@@ -79,6 +79,12 @@ std::string plan_name(const Q4Plan& p) {
         snprintf(buf, sizeof buf, "skinny-s%d", p.splits);
         return buf;
     case kPlanGemm: return "gemm";
+    case kPlanBig:
+        snprintf(buf, sizeof buf, "big-s%d", p.splits);
+        return buf;
+    case kPlanWide:
+        snprintf(buf, sizeof buf, "wide-s%d", p.splits);
+        return buf;
     default: return "none";
     }
 }
@@ -126,7 +132,7 @@ void load_cache(Tuner& t) {
         std::string key, name;
         PlanEntry e;
         if (!(in >> key >> e.plan.kind >> e.plan.tile >> e.plan.splits >> name)) continue;
-        if (e.plan.kind < kPlanGeneric || e.plan.kind > kPlanGemm || name != plan_name(e.plan)) continue;
+        if (e.plan.kind < kPlanGeneric || e.plan.kind > kPlanLast || name != plan_name(e.plan)) continue;
         e.name = name;
         e.from_cache = true;
         t.cached[key] = e;
@@ -177,6 +183,10 @@ std::vector<Candidate> candidates(int mt, int x_dtype) {
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanPipe, tile, sp}, 3e-3f});
         if (mt <= 32)
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanSkinny, 0, sp}, 3e-3f});
+        if (mt > 32) {
+            for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanBig, 0, sp}, 3e-3f});
+            for (int sp : {0, 1, 2}) c.push_back({{kPlanWide, 0, sp}, 3e-3f});
+        }
     }
     c.push_back({{kPlanGemm, 0, 0}, 3e-3f});
     return c;

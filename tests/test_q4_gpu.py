@@ -139,6 +139,7 @@ def test_q4_gemm_tiles(hip, oracle, monkeypatch, tile, shape):
     monkeypatch.setenv("BYHIP_Q4_TILE", str(tile))
     monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
     monkeypatch.setenv("BYHIP_Q4_SKINNY_MAX_M", "0")  # the LDS-staged kernel for every M
+    monkeypatch.setenv("BYHIP_Q4_PREFILL", "1")
     g = synth.rng(7000 + 17 * M + N)
     wq, sc, ze, _ = synth.q4_weights(g, N, K)
     x = synth.activations(g, M, K, np.float16)
@@ -160,6 +161,7 @@ def test_q4_gemm_split_k(hip, oracle, monkeypatch, splits, shape, y_dtype):
     monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
     monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
     monkeypatch.setenv("BYHIP_Q4_SKINNY_MAX_M", "0")  # the LDS-staged kernel for every M
+    monkeypatch.setenv("BYHIP_Q4_PREFILL", "1")
     g = synth.rng(7100 + 13 * M + N + splits)
     wq, sc, ze, _ = synth.q4_weights(g, N, K)
     x = synth.activations(g, M, K, np.float16)
@@ -181,8 +183,8 @@ def test_q4_gemm_split_k(hip, oracle, monkeypatch, splits, shape, y_dtype):
 @pytest.mark.parametrize("group", [32, 128, 0])
 def test_q4_gemm_skinny(hip, oracle, monkeypatch, M, splits, group):
     """The skinny small-M kernel (weights straight to MFMA registers, K split over the block's
-    waves): 16-, 32- and 64-row blocks, ragged M and N, groups 32 / 128 / whole row, with and
-    without split-K, fp16 in and out, against the oracle."""
+    waves): 16- and 32-row blocks, ragged M and N, groups 32 / 128 / whole row, with and without
+    split-K, fp16 in and out, against the oracle; M above 32 takes the prefill route."""
     from bybylang_amd import synth
     K, N = 768, 200
     monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
@@ -196,6 +198,56 @@ def test_q4_gemm_skinny(hip, oracle, monkeypatch, M, splits, group):
     got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
     want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, group, gpr)
     tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("kind", ["big", "wide"])
+@pytest.mark.parametrize("shape", [(130, 768, 520), (40, 512, 136), (256, 1024, 264), (64, 384, 128)])
+@pytest.mark.parametrize("splits", [0, 3])
+@pytest.mark.parametrize("group", [32, 128, 0])
+def test_q4_gemm_prefill_tiles(hip, oracle, monkeypatch, kind, shape, splits, group):
+    """The prefill kernels (forced through BYHIP_Q4_PREFILL): the 128 x 256 tile (activations
+    shared through LDS, weights straight to MFMA registers) and the 64 x 128 skinny tile (K split
+    over the block's waves); ragged M and N, groups 32 / 128 / whole row, with and without split-K,
+    fp16 in and out, against the oracle; a repeat call is bit-identical."""
+    from bybylang_amd import synth
+    M, K, N = shape
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_SKINNY_MAX_M", "0")
+    monkeypatch.setenv("BYHIP_Q4_PREFILL", "2" if kind == "big" else "3")
+    if splits:
+        monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
+    g = synth.rng(7500 + 11 * M + N + group + splits)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K, group if group else K)
+    gpr = K // group if group else 1
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 prefill {kind} M={M} K={K} N={N} splits={splits} group={group}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    again, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    assert np.array_equal(got, again)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, group, gpr)
+    tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("kind", ["big", "wide"])
+@pytest.mark.parametrize("y_dtype", ["F32", "BF16"])
+def test_q4_gemm_prefill_out_dtypes(hip, oracle, monkeypatch, kind, y_dtype):
+    """fp32 and bf16 outputs of the prefill kernels (the fp32 path also through split-K)."""
+    from bybylang_amd import synth
+    M, K, N = 200, 1024, 300
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_PREFILL", "2" if kind == "big" else "3")
+    if y_dtype == "F32":
+        monkeypatch.setenv("BYHIP_Q4_SPLIT", "2")
+    g = synth.rng(7600 + len(kind) + len(y_dtype))
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 prefill {kind} y={y_dtype}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, getattr(hip, y_dtype))
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    if y_dtype == "BF16":
+        tier_check(got, f32_to_bf16_rne(want).reshape(M, N), TIER_BF16_OUT)
+    else:
+        tier_check(got, want, TIER_F32_ACC)
 
 
 @pytest.mark.parametrize("M", [32, 256])

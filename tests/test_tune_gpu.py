@@ -58,9 +58,11 @@ def test_prepare_decode_and_prefill(hip, oracle, plans):
         assert hip.q4_prepare(w, M_tune, hip.F16) == 0
         name, cached = hip.q4_plan_info(w, M_tune, hip.F16)
         assert not cached
-        assert name == "generic" or name == "gemm" or name.startswith("pipe-") or name.startswith("skinny-")
+        assert name in ("generic", "gemm") or name.split("-")[0] in ("pipe", "skinny", "big", "wide")
         if M_tune > 32:
             assert not name.startswith("skinny-")
+        else:
+            assert not name.startswith(("big-", "wide-"))
         for M in Ms:
             assert hip.q4_plan_info(w, M, hip.F16)[0] == name  # one plan per class
             x = synth.activations(g, M, K, np.float16)
