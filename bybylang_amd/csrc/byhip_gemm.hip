@@ -823,28 +823,37 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
             for (int i = 0; i < kBigFM; ++i)
                 xv[kk & 1][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
         };
-        xread(0);
+        // Unit u = (kk, j) = (u / 4, u % 4): fragment j's weights of MFMA column kk against the 8
+        // row fragments. The weights of unit u + 1 are dequantized before unit u's MFMAs are
+        // issued, so the compiler can interleave that VALU work with them (explicit scheduling
+        // groups of one MFMA and two VALU instructions measured slower: hazard waits).
+        auto dequant = [&](int u) {
+            const uint32_t d = r.w[u & 3][u >> 2];
+            uint32_t q[4];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            h8 ax[kBigFM];
-#pragma unroll
-            for (int i = 0; i < kBigFM; ++i) ax[i] = *reinterpret_cast<const h8*>(&xv[kk & 1][i]);
-            if (kk < 3) xread(kk + 1);
-#pragma unroll
-            for (int j = 0; j < kBigFN; ++j) {
-                const uint32_t d = r.w[j][kk];
-                uint32_t q[4];
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const uint32_t rep = __builtin_amdgcn_perm(d, d, 0x01010101u * (uint32_t)b);
-                    q[b] = h2_bits((bits_h2((rep & 0x00F0000Fu) | mag) - zz) * ss[j]);
-                }
-                const uint4 u = make_uint4(q[0], q[1], q[2], q[3]);
-                const h8 bw = *reinterpret_cast<const h8*>(&u);
-#pragma unroll
-                for (int i = 0; i < kBigFM; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw, acc[i][j], 0, 0, 0);
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t rep = __builtin_amdgcn_perm(d, d, 0x01010101u * (uint32_t)b);
+                q[b] = h2_bits((bits_h2((rep & 0x00F0000Fu) | mag) - zz) * ss[u & 3]);
             }
+            const uint4 v = make_uint4(q[0], q[1], q[2], q[3]);
+            return *reinterpret_cast<const h8*>(&v);
+        };
+        xread(0);
+        h8 ax[kBigFM];
+        h8 bw = dequant(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int kk = u >> 2, j = u & 3;
+            if (j == 0) {
+#pragma unroll
+                for (int i = 0; i < kBigFM; ++i) ax[i] = *reinterpret_cast<const h8*>(&xv[kk & 1][i]);
+                if (kk < 3) xread(kk + 1);
+            }
+            const h8 bn = u < 15 ? dequant(u + 1) : bw;
+#pragma unroll
+            for (int i = 0; i < kBigFM; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw, acc[i][j], 0, 0, 0);
+            bw = bn;
         }
     };
 
