@@ -151,7 +151,7 @@ def bench_c3(dev, synth, steps, warmup):
 C4_OPS = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 2 * 14336), ("down", 14336, 4096)]
 
 
-def bench_c4(dev, synth, steps, warmup):
+def bench_c4(dev, synth, steps, warmup, tuned=False):
     out = {}
     layer_bytes = {M: sum(q4_bytes(M, K, N) for _, K, N in C4_OPS) for M in (1, 32, 256)}
     copies = max(1, -(-ROTATE_BYTES // layer_bytes[1]))
@@ -181,7 +181,7 @@ def bench_c4(dev, synth, steps, warmup):
         flops = sum(2 * M * K * N for _, K, N in C4_OPS)
         out[f"M{M}"] = {"per_op": per_op, "batch_us": per * 1e6,
                         "batch_GBps": layer_bytes[M] / per / 1e9, "batch_TFLOPs": flops / per / 1e12}
-        if M > 1:
+        if tuned and M > 1:
             # residentPrepareQ4 for each projection at this M (plans tuned outside the timed region,
             # into a fresh plan directory), then the same batch again
             import tempfile
@@ -370,7 +370,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="c1,c2,c3,c4,up",
-                    help="configurations to measure (c1 is the headline and always runs)")
+                    help="configurations to measure (c1 is the headline and always runs); c4t is c4 "
+                         "with the batch timed again after byhip_q4_prepare tunes each projection")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run the copy kernel on MIB MiB (calibration for counter runs)")
@@ -396,8 +397,9 @@ def main() -> int:
         configs["c2_prefill_q4_gemm"] = bench_c2(dev, synth, args.steps, args.warmup)
     if "c3" in wanted:
         configs["c3_mxfp4_gemm"] = bench_c3(dev, synth, args.steps, args.warmup)
-    if "c4" in wanted:
-        configs["c4_layer_batch"] = bench_c4(dev, synth, max(1, args.steps // 5), max(0, args.warmup // 5))
+    if "c4" in wanted or "c4t" in wanted:
+        configs["c4_layer_batch"] = bench_c4(dev, synth, max(1, args.steps // 5), max(0, args.warmup // 5),
+                                             tuned="c4t" in wanted)
     if "up" in wanted:
         configs["resident_upload_mapped"] = bench_upload_mapped(synth)
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None

@@ -10,6 +10,11 @@
         library's copy kernel (copy_words) moving N bytes in the same run, so the figure is in the
         units of a known transfer: factor = N / (counter KiB * 1024) for reads and for writes.
 
+    python -m bybylang_amd.profile_summary counters DB [DB ...] --kernel SUBSTRING
+        for each kernel whose name contains SUBSTRING: the average per dispatch of every counter
+        in the databases (summed over the counter's instances: XCDs, SEs, CUs), and the average
+        dispatch duration
+
 The databases are the *_results.db files rocprofv3 writes with -d/-o.
 """
 from __future__ import annotations
@@ -66,6 +71,29 @@ def traffic(fetch_db: str, write_db: str, copy_bytes: int, kernel: str) -> dict:
             "traffic_bytes": kf * 1024.0 * ff + kw * 1024.0 * fw}
 
 
+def counters(dbs, kernel: str) -> dict:
+    """{kernel name: {"dispatches": n, "avg_us": duration, counter: average per dispatch}}"""
+    out = collections.defaultdict(dict)
+    for db in dbs:
+        con = sqlite3.connect(db)
+        rows = con.execute("select dispatch_id, kernel_name, counter_name, value, duration "
+                           "from counters_collection").fetchall()
+        con.close()
+        per = collections.defaultdict(lambda: collections.defaultdict(lambda: collections.defaultdict(float)))
+        dur = collections.defaultdict(dict)
+        for d, k, c, v, du in rows:
+            if kernel in k:
+                per[k][c][d] += v
+                dur[k][d] = du
+        for k, cs in per.items():
+            ds = list(dur[k].values())
+            out[k]["dispatches"] = len(ds)
+            out[k].setdefault("avg_us", sum(ds) / len(ds) / 1e3)
+            for c, byd in cs.items():
+                out[k][c] = sum(byd.values()) / len(byd)
+    return dict(out)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -77,7 +105,16 @@ def main(argv=None) -> int:
     r.add_argument("--copy-bytes", type=int, required=True)
     r.add_argument("--kernel", required=True)
     r.add_argument("--json")
+    c = sub.add_parser("counters")
+    c.add_argument("dbs", nargs="+")
+    c.add_argument("--kernel", required=True)
     a = ap.parse_args(argv)
+    if a.cmd == "counters":
+        for name, vals in counters(a.dbs, a.kernel).items():
+            print(f"`{name[:110]}`: {vals['dispatches']} dispatches, {vals['avg_us']:.2f} us")
+            for k in sorted(v for v in vals if v not in ("dispatches", "avg_us")):
+                print(f"  {k} = {vals[k]:.4g}")
+        return 0
     if a.cmd == "trace":
         print(f"| kernel | dispatches | avg us | min us | max us |\n|---|---:|---:|---:|---:|")
         for name, n, avg, mn, mx in kernel_durations(a.db):
