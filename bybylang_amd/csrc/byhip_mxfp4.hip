@@ -228,7 +228,8 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         constexpr int P = decltype(Pc)::value;
         constexpr int T1 = (P + 1) & 3;
         constexpr bool batch = P & 1, scales = P == 1;
-        constexpr int V = (batch ? 2 * kPairDma : 0) + (scales ? kScaleDma : 0);
+        // loads issued after the ones step s + 1 reads: this step's batch and scales
+        constexpr int V = (batch ? kPairDma : 0) + (scales ? kScaleDma : 0);
         if constexpr (batch) {
             if (scales) dma_scales((s + 3) >> 2, sdst);
 #pragma unroll
