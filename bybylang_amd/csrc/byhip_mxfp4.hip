@@ -386,7 +386,9 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
                     }
                     o = make_uint4(w[0], w[1], w[2], w[3]);
                 }
-                *reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.y) + ((size_t)m * N + n) * es) = o;
+                // streamed out (nontemporal): nothing reads the output back in this kernel
+                const v4u ov = {o.x, o.y, o.z, o.w};
+                __builtin_nontemporal_store(ov, reinterpret_cast<v4u*>(static_cast<uint8_t*>(a.y) + ((size_t)m * N + n) * es));
             } else {
 #pragma unroll
                 for (int e = 0; e < per; ++e)
