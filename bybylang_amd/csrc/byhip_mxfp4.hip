@@ -72,19 +72,17 @@ __device__ __forceinline__ i8v operand(uint4 u) {
     return (i8v){(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
 }
 
-// One wave's operands of one K step: 8 x fragments, 8 W fragments and their scale bytes, two per
-// register: fragment 2 k in byte 0 and 2 k + 1 in byte 2 of sa[k] / sb[k] (the MFMA's op_sel picks
-// the byte).
+// One wave's operands of one K step: 8 x fragments, 8 W fragments and their scale bytes, one per
+// register in byte 0 (a byte load each, so no ALU op combines them and nothing waits for them
+// before the MFMAs that use them).
 struct Frags {
     uint4 a[8], b[8];
-    int sa[4], sb[4];
+    int sa[8], sb[8];
 };
 
-// acc += a . b with the scale bytes of fragments i and j (compile-time parities pick the byte).
-template <int PI, int PJ>
+// acc += a . b with the scale bytes of the two fragments (byte 0 of sa and sb: op_sel 0).
 __device__ __forceinline__ f4 mx_mfma(uint4 a, uint4 b, f4 acc, int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(operand(a), operand(b), acc, 4, 4, 2 * PI, sa,
-                                                              2 * PJ, sb);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(operand(a), operand(b), acc, 4, 4, 0, sa, 0, sb);
 }
 
 // Workgroup barrier after this wave's LDS reads and all but the newest N direct loads have
@@ -168,8 +166,10 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            f.sa[k] = (int)sbuf[sa_row + 512 * k + 4 * T] | ((int)sbuf[sa_row + 512 * k + 256 + 4 * T] << 16);
-            f.sb[k] = (int)sbuf[sb_row + 512 * k + 4 * T] | ((int)sbuf[sb_row + 512 * k + 256 + 4 * T] << 16);
+            f.sa[2 * k] = sbuf[sa_row + 512 * k + 4 * T];
+            f.sa[2 * k + 1] = sbuf[sa_row + 512 * k + 256 + 4 * T];
+            f.sb[2 * k] = sbuf[sb_row + 512 * k + 4 * T];
+            f.sb[2 * k + 1] = sbuf[sb_row + 512 * k + 256 + 4 * T];
         }
     };
 
@@ -186,8 +186,10 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         if (g == 0) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                f.sa[k] = (int)sbuf[sa_row + 512 * k + 4 * T] | ((int)sbuf[sa_row + 512 * k + 256 + 4 * T] << 16);
-                f.sb[k] = (int)sbuf[sb_row + 512 * k + 4 * T] | ((int)sbuf[sb_row + 512 * k + 256 + 4 * T] << 16);
+                f.sa[2 * k] = sbuf[sa_row + 512 * k + 4 * T];
+                f.sa[2 * k + 1] = sbuf[sa_row + 512 * k + 256 + 4 * T];
+                f.sb[2 * k] = sbuf[sb_row + 512 * k + 4 * T];
+                f.sb[2 * k + 1] = sbuf[sb_row + 512 * k + 256 + 4 * T];
             }
         }
     };
@@ -241,13 +243,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         for (int i = 0; i < 2; ++i) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int sa = cur.sa[i >> 1], sb = cur.sb[j >> 1];
-                if (i & 1)
-                    acc[i][j] = (j & 1) ? mx_mfma<1, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<1, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
-                else
-                    acc[i][j] = (j & 1) ? mx_mfma<0, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<0, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
+                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -261,13 +257,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         for (int i = 2; i < 4; ++i) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int sa = cur.sa[i >> 1], sb = cur.sb[j >> 1];
-                if (i & 1)
-                    acc[i][j] = (j & 1) ? mx_mfma<1, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<1, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
-                else
-                    acc[i][j] = (j & 1) ? mx_mfma<0, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<0, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
+                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -281,13 +271,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         for (int i = 4; i < 6; ++i) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int sa = cur.sa[i >> 1], sb = cur.sb[j >> 1];
-                if (i & 1)
-                    acc[i][j] = (j & 1) ? mx_mfma<1, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<1, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
-                else
-                    acc[i][j] = (j & 1) ? mx_mfma<0, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<0, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
+                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -301,13 +285,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         for (int i = 6; i < 8; ++i) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int sa = cur.sa[i >> 1], sb = cur.sb[j >> 1];
-                if (i & 1)
-                    acc[i][j] = (j & 1) ? mx_mfma<1, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<1, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
-                else
-                    acc[i][j] = (j & 1) ? mx_mfma<0, 1>(cur.a[i], cur.b[j], acc[i][j], sa, sb)
-                                        : mx_mfma<0, 0>(cur.a[i], cur.b[j], acc[i][j], sa, sb);
+                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
