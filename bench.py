@@ -348,6 +348,28 @@ def measured_traffic():
         return None
 
 
+def bench_read_probe(dev):
+    """byhip_debug_read, the plain streaming read the kernels' reads are compared with: over 1 GiB
+    (the steady rate), and over config 1's bytes per launch (33,067,008 B) rotating through 32
+    slices of that buffer, timed like config 1 (recorded launches, each reading cold)."""
+    from bybylang_amd import _abi
+    lib = _abi.load()
+    big, sink = dev.DeviceBuffer(1 << 30), dev.DeviceBuffer(1 << 20)
+    out = {}
+    fn = lambda i: _abi.check(lib.byhip_debug_read(big.ptr, 1 << 30, sink.ptr, 1 << 20))  # noqa: E731
+    gpu_s, _ = run_steps(fn, 10, 2)
+    out["steady_1GiB_GBps"] = (1 << 30) / (gpu_s / 10) / 1e9
+    part = q4_bytes(1, 4096, 14336)
+    fn = lambda i: _abi.check(lib.byhip_debug_read(big.ptr + (i % 32) * part, part, sink.ptr, 1 << 20))  # noqa: E731
+    gpu_s, _ = run_steps(fn, 200, 32)
+    out["per_launch_c1_bytes"] = part
+    out["per_launch_us"] = gpu_s / 200 * 1e6
+    out["per_launch_GBps"] = part / (gpu_s / 200) / 1e9
+    big.close()
+    sink.close()
+    return out
+
+
 def copy_probe(mib: int, times: int = 10):
     """Runs the library's copy kernel on `mib` MiB device to device `times` times: the known
     transfer that a counter run scales FETCH_SIZE / WRITE_SIZE by."""
@@ -369,7 +391,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,up",
+    ap.add_argument("--configs", default="c1,c2,c3,c4,up,rp",
                     help="configurations to measure (c1 is the headline and always runs); c4t is c4 "
                          "with the batch timed again after byhip_q4_prepare tunes each projection")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -402,6 +424,8 @@ def main() -> int:
                                              tuned="c4t" in wanted)
     if "up" in wanted:
         configs["resident_upload_mapped"] = bench_upload_mapped(synth)
+    if "rp" in wanted:
+        configs["hbm_read_probe"] = bench_read_probe(dev)
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
 
     per_s = c1["us_per_step"] * 1e-6

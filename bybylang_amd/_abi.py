@@ -92,6 +92,7 @@ SIGNATURES = {
     "byhip_debug_unpack_q4": (_I, [_VP, _U8P, _FP, _FP]),
     "byhip_debug_unpack_fp4km": (_I, [_U8P, _SZ, _FP, _SZ, _I, _I, _U8P, _FP]),
     "byhip_debug_copy": (_I, [_VP, _VP, _SZ]),
+    "byhip_debug_read": (_I, [_VP, _SZ, _VP, _SZ]),
 }
 
 _lib = None

@@ -537,7 +537,46 @@ __global__ __launch_bounds__(256) void copy_words(const uint4* __restrict__ src,
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         dst[i] = src[i];
 }
+// Streaming read: each wave reads runs of 8 x 1 KB (a 16-byte nontemporal load per lane, eight in
+// flight), grid-stride; the tail words one per thread. Each wave stores its fold of the words to its
+// own sink slot, which keeps the loads.
+constexpr int kReadDepth = 8;
+__global__ __launch_bounds__(256) void read_words(const uint4* __restrict__ src, size_t n, uint32_t* sink) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u* s4 = reinterpret_cast<const v4u*>(src);
+    const size_t wave = (size_t)blockIdx.x * 4 + threadIdx.x / 64, nwaves = (size_t)gridDim.x * 4;
+    const size_t lane = threadIdx.x & 63, run = 64 * kReadDepth;
+    uint32_t acc = 0;
+    for (size_t seg = wave; seg < n / run; seg += nwaves) {
+        v4u v[kReadDepth];
+#pragma unroll
+        for (int d = 0; d < kReadDepth; ++d) v[d] = __builtin_nontemporal_load(s4 + seg * run + 64 * d + lane);
+#pragma unroll
+        for (int d = 0; d < kReadDepth; ++d) acc ^= v[d][0] + v[d][1] + v[d][2] + v[d][3];
+    }
+    for (size_t i = n / run * run + (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        acc ^= src[i].x;
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    if (lane == 0) sink[wave] = acc;
+}
 }  // namespace
+
+extern "C" int byhip_debug_read(const void* src, size_t bytes, void* sink, size_t sink_bytes) {
+    return guard([&] {
+        enter_compute();
+        if (bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+            fail("byhip: read needs a 16-byte aligned pointer and size");
+        const unsigned grid = (unsigned)compute_units() * 4;  // 16 waves per CU
+        if (sink_bytes < (size_t)grid * 4 * sizeof(uint32_t))
+            fail("byhip: read sink needs %zu bytes", (size_t)grid * 4 * sizeof(uint32_t));
+        check_span(src, bytes, "read source");
+        check_span(sink, (size_t)grid * 4 * sizeof(uint32_t), "read sink");
+        if (bytes == 0) return;
+        hipLaunchKernelGGL(read_words, dim3(grid), dim3(256), 0, stream(), static_cast<const uint4*>(src),
+                           bytes / 16, static_cast<uint32_t*>(sink));
+        BYHIP_LAUNCHED("read_words");
+    });
+}
 
 extern "C" int byhip_debug_copy(void* dst, const void* src, size_t bytes) {
     return guard([&] {

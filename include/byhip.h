@@ -257,6 +257,11 @@ int byhip_debug_unpack_fp4km(const uint8_t* blob, size_t scale_base, const float
 /* A plain device copy of `bytes` (16-byte multiples): the reference point for HBM bandwidth and
  * for scaling hardware traffic counters. No counterpart in the reference. */
 int byhip_debug_copy(void* dst, const void* src, size_t bytes);
+/* A plain streaming read of `bytes` (16-byte multiples; nontemporal 16-byte loads, eight per lane
+ * in flight, 16 waves per CU): the reference point for what the kernels' reads can reach. Each
+ * wave stores a fold of what it read into `sink`, which must hold 16 * CUs 32-bit words.
+ * No counterpart in the reference. */
+int byhip_debug_read(const void* src, size_t bytes, void* sink, size_t sink_bytes);
 
 #ifdef __cplusplus
 }
