@@ -29,6 +29,8 @@ struct GemmArgs {
     float zero_value = 0.0f;
     int group = 0;                 // 0: one group per row
     int gpr = 0;
+    const void* sblk = nullptr;    // fp16 scales per 32-value chunk in blocks of 8 columns,
+                                   // [ceil(N/8)][K/32][8] (byhip_q4w::sblk), or null
     // FP4-KM
     const uint8_t* blob = nullptr;
     size_t scale_base = 0;

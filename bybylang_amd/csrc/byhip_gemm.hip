@@ -532,7 +532,12 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
     // offsets below 2^31).
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
     const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
-    const rsrc_t sr = make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
+    // Scales: from the blocked copy when there is one (a lane group's 4 chunks of 8 columns are 64
+    // contiguous bytes, so a fragment's load touches 2 lines rather than 16), else row-major.
+    const bool sblk = a.sblk != nullptr;
+    const uint32_t G = (uint32_t)K >> 5;
+    const rsrc_t sr = sblk ? make_rsrc(a.sblk, (uint32_t)(((size_t)a.N + 7) / 8 * 8 * G * 2))
+                           : make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
     const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
     // Direct load u of a step: lane -> row 4u + lane / 16, LDS slot lane % 16 holding chunk
     // slot ^ (row & 15) of that row. Loads u and u + 4 differ by 16 rows and share the slot
@@ -546,8 +551,10 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
     }
     const uint32_t xrow16 = 16u * (uint32_t)K * 2u;  // 16 activation rows
     const uint32_t wo = (uint32_t)(n0 + c) * (uint32_t)a.row_bytes + 16u * g;
-    const uint32_t so = (uint32_t)(n0 + c) * (uint32_t)a.gpr;
-    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes, sfrag = 32u * (uint32_t)a.gpr;  // per fragment
+    const uint32_t so = sblk ? 2u * ((((uint32_t)n0 >> 3) + ((uint32_t)c >> 3)) * G * 8u + 8u * g + (c & 7))
+                             : (uint32_t)(n0 + c) * (uint32_t)a.gpr;
+    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes;                              // per fragment
+    const uint32_t sfrag = sblk ? 32u * G : 32u * (uint32_t)a.gpr;
     uint8_t* const xbuf = lds + wid * 2 * XBUF;
 
     // Step t of this wave is block step (wid + 4t + rot) mod nsteps. For the narrow tiles the
@@ -569,6 +576,7 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
         const uint32_t k0 = (uint32_t)(s_first + (ok ? kstep(t) : 0)) * 128u;
         const uint32_t oob = ok ? 0u : 0x80000000u;
         const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
+        const uint32_t soff = sblk ? so + 16u * (k0 >> 5) : 2u * (so + grp);
 #pragma unroll
         for (int u = 0; u < XDMA; ++u)
             lds_dma16(xr, dst + 1024 * u, xo[u & 3] + 2u * k0, oob + (uint32_t)(u >> 2) * xrow16);
@@ -577,7 +585,7 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
             r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 2);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (so + grp), oob + (uint32_t)j * sfrag, 0);
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, oob + (uint32_t)j * sfrag, 0);
     };
 
     const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
@@ -756,7 +764,11 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
     // offset, with the rows and columns the tile reaches past M and N, below 2^31).
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
     const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
-    const rsrc_t sr = make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
+    // Scales from the blocked copy when there is one (2 lines per fragment load), else row-major.
+    const bool sblk = a.sblk != nullptr;
+    const uint32_t G = (uint32_t)K >> 5;
+    const rsrc_t sr = sblk ? make_rsrc(a.sblk, (uint32_t)(((size_t)a.N + 7) / 8 * 8 * G * 2))
+                           : make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
     const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
 
     // Direct load u (0..7) of wave w: lane -> row 32w + 4u + lane / 16, LDS slot lane % 16 holding
@@ -771,8 +783,8 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
     const uint32_t xrow16 = 16u * (uint32_t)K * 2u;
     const int ncol = n0 + 64 * wid + c;
     const uint32_t wo = (uint32_t)ncol * (uint32_t)a.row_bytes + 16u * g;
-    const uint32_t so = (uint32_t)ncol * (uint32_t)a.gpr;
-    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes, sfrag = 32u * (uint32_t)a.gpr;
+    const uint32_t so = sblk ? 2u * (((uint32_t)ncol >> 3) * G * 8u + 8u * g + (ncol & 7)) : (uint32_t)ncol * (uint32_t)a.gpr;
+    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes, sfrag = sblk ? 32u * G : 32u * (uint32_t)a.gpr;
     uint8_t* const xdst = lds + 32 * 256 * wid;  // this wave's rows of each buffer
 
     // A step past the block's last one adds 2^31 through the scalar offset: every resource rejects
@@ -782,6 +794,7 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
         const uint32_t k0 = (uint32_t)(s_first + (ok ? t : 0)) * 128u;
         const uint32_t oob = ok ? 0u : 0x80000000u;
         const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
+        const uint32_t soff = sblk ? so + 16u * (k0 >> 5) : 2u * (so + grp);
         uint8_t* const dst = xdst + buf * kBigBuf;
 #pragma unroll
         for (int u = 0; u < kBigM / 16; ++u)
@@ -791,7 +804,7 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
             r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 2);
 #pragma unroll
         for (int j = 0; j < kBigFN; ++j)
-            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2u * (so + grp), oob + (uint32_t)j * sfrag, 0);
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, oob + (uint32_t)j * sfrag, 0);
     };
 
     // Natural-order dequantization: v_perm_b32 copies byte b of the word (values 2b, 2b + 1) to

@@ -282,6 +282,7 @@ GemmArgs q4_gemm_args(const void* x, int x_dtype, const byhip_q4w* w, void* y, i
     a.M = M; a.K = w->K; a.N = w->N;
     a.wq = w->wq; a.row_bytes = w->row_bytes; a.scales = w->scales; a.scale_f16 = w->scale_f16;
     a.zeros = w->zeros; a.zero_value = w->zero_value; a.group = w->group; a.gpr = w->gpr;
+    a.sblk = w->blk_scale_f16 ? w->sblk : nullptr;
     return a;
 }
 
