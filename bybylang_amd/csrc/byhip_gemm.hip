@@ -675,8 +675,8 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
         __builtin_amdgcn_sched_barrier(0);
     };
     if constexpr (FN > 4) {
-        // One step per iteration, the next step's registers copied over: with 128 accumulators the
-        // register allocator keeps them in place only in a single-step loop body.
+        // Two steps per iteration and no early exit: with 128 accumulators an early exit (or a
+        // single-step body) makes the register allocator move them between AGPRs every iteration.
         for (int t = 0; t < nt; t += 2) {
             step(t, ra, rb, xbuf, xbuf + XBUF);
             step(t + 1, rb, ra, xbuf + XBUF, xbuf);
