@@ -478,14 +478,17 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 
 // Skinny Q4 GEMM for small M (the decode-batch and short-prefill shapes): weights are read once,
 // straight from HBM into MFMA operand registers, so the kernel streams them like the GEMV while the
-// MFMAs do the row products. Same format conditions as q4_gemm_pipe, K % 128 == 0, M <= 32.
+// MFMAs do the row products. Same format conditions as q4_gemm_pipe, K % 128 == 0, M <= 32; the
+// wide 64 x 128 tile below serves prefill shapes.
 //   Block: 4 waves on the same 16 FN columns (FN fragments of 16) and BM rows (BM / 16
 //   fragments);
 //   the block's K steps of 128 are dealt round-robin to its waves, and the four partial tiles are
 //   added through LDS at the end (wave order 0 + 1 + 2 + 3).
 //   K order: in MFMA kk (0..3) of a step, lane group g (lanes 16g..16g+15) supplies the values
 //   32g + 8kk + (0, 4, 1, 5, 2, 6, 3, 7) of the step. A lane's weights for a step are then one
-//   16-byte load (one 32-value group, one scale); the (k, k+4) order is what the AND-OR
+//   16-byte load (one 32-value group) and one scale, from the blocked scale copy when the
+//   weights have one (a fragment's 16 columns x 4 chunks are then 2 lines); the (k, k+4) order is
+//   what the AND-OR
 //   dequantization yields, and perm8 gives the activations the same order. Both operands use it,
 //   so every product pairs the same k.
 //   Activations: each wave moves its step's BM x 128 slice straight from global memory into its
@@ -716,9 +719,9 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
 }
 
 // Large-tile Q4 GEMM for prefill: a 128 x 256 tile per block, so each activation byte is read once
-// per 256 columns and each weight byte once per 128 rows. Every operand byte reaches the CU through
-// its vector L1, whose miss handling (outstanding line fills times L2 latency) is what bounds the
-// smaller tiles at these shapes; the larger tile needs about half the bytes per output.
+// per 256 columns and each weight byte once per 128 rows. Every operand byte reaches the CU as an
+// L1-to-L2 request, and the bytes each CU must pull that way bound the smaller tiles at these
+// shapes; the larger tile needs about half the bytes per output.
 //   Block: 4 waves; wave w owns columns 64w .. 64w+63 of the tile and all 128 rows (8 x 4
 //   fragments, 128 accumulators), and the block shares the activation tile.
 //   K steps of 128: in MFMA kk (0..3) lane group g supplies values 32g + 8kk .. 32g + 8kk + 7 in
