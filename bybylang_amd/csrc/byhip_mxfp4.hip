@@ -1,24 +1,35 @@
-// byhip_mxfp4.hip - native MXFP4 GEMM on gfx950's scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4).
+// byhip_mxfp4.hip - native MXFP4 GEMM on gfx950's scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4).
 //
 // y[M, N] = x[M, K] . W^T with both operands E2M1 (fp4) and one E8M0 scale per 32 values, fp32
 // accumulation. Operand layout (checked on the device): lane l holds the 32 values of row (or
-// column) l%16, K block l/16 of the 128-deep step as 16 bytes, low nibble first, and its scale in
-// the byte of the scale register that op_sel names. One FP4-KM group (16 bytes + 1 scale byte,
-// session_vm.nim:384-388) is therefore exactly one lane's operand. FP4-KM stores element j and
-// j+16 in byte j rather than elements 2j and 2j+1, so the MFMA sees the 32 values of a group in a
-// permuted order; x uses the same packing, both operands carry the same permutation, and the dot
-// product is unchanged.
+// column) l%32 of one 32-value K block as 16 bytes, low nibble first, and its scale in the byte of
+// the scale register that op_sel names; the two lane halves cover two K blocks, so one MFMA is 64
+// deep. One FP4-KM group (16 bytes + 1 scale byte, session_vm.nim:384-388) is therefore exactly
+// one lane's operand. FP4-KM stores element j and j+16 in byte j rather than elements 2j and 2j+1,
+// so the MFMA sees the 32 values of a group in a permuted order; x uses the same packing, both
+// operands carry the same permutation, and the dot product is unchanged.
 //
-// Tiling: a 256-thread block computes a 256 x 256 tile, each wave a 128 x 128 quarter as 8 x 8
-// fragments (64 accumulators of 4 floats). Per 128-deep K step the block moves 256 rows x 64 bytes
-// of x and of W straight from global memory into LDS (gfx950's 16-byte buffer_load ... lds, no
-// staging registers), 4 lanes per 64-byte row segment, into a swizzled layout; the scale bytes
-// follow once per 4 steps, 16 bytes per row. Steps are loaded in pairs, the two 64-byte halves of
-// each row's 128-byte line a few loads apart, which halves the line fetches. Four LDS stages
-// overlap, during the MFMAs of step s, the LDS reads of step s + 1 and the direct loads of the
-// next pair, with one LDS barrier per step; the loads and reads are spread over the step's MFMAs
-// in quarters. The output tile leaves through LDS so that global stores are 16 bytes per lane
-// along rows.
+// Why 32x32x64: on the MI355X the 16x16x128 form sustains about 4.6 PFLOP/s with one wave per
+// SIMD and the 32x32x64 form about 6.8 (register-only throughput, measured during development).
+//
+// Tiling: a 256-thread block computes a 256 x 256 tile, each wave a 128 x 128 quarter as 4 x 4
+// fragments of 32 x 32 (16 accumulators of 16 floats). A K step is 128 deep: per fragment two
+// MFMAs, one per 64-deep half. The block moves x and W straight from global memory into LDS
+// (gfx950's 16-byte buffer_load ... lds, no staging registers). One direct load covers 8 rows x
+// 128 bytes, whole cache lines: two steps of each row. Fetching whole lines doubles what a CU pulls
+// per cycle against half lines (136 against 67 GB/s per CU from L2 in a standalone probe). The
+// scale bytes follow once per 4 steps, 16 bytes per row. LDS holds two regions of two steps each;
+// during the MFMAs of step s the wave reads step s + 1's operands, and odd steps issue the loads
+// of the pair after next. One LDS barrier per pair. Reads and loads sit between the MFMAs, so the
+// MFMA pipe is fed while they issue. The output tile leaves through LDS so that global stores are
+// 16 bytes per lane along rows.
+//
+// The MFMAs are inline assembly, which keeps the 256 accumulators in place in AGPRs (the
+// compiler's own MFMA shuffled them through VGPRs in this loop). The compiler then does not know
+// them as MFMAs, so the code covers what it would otherwise track: the accumulators are zeroed and
+// settled before the first MFMA, each step's operand registers stay reserved until the step ends,
+// and the results are waited out before they are read. Register dependencies of the operands
+// (LDS reads feeding an MFMA) are tracked by the compiler as for any instruction.
 //
 // Tile order: blocks are handed to the 8 XCDs round-robin; block b works on tile
 // (b % 8) * ceil(T/8) + b / 8 in column-major tile order, so each XCD owns a run of column tiles and
@@ -35,6 +46,7 @@ constexpr int KSTEP = 128;            // values per step (4 groups)
 constexpr int kXcds = 8;
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
 
 struct MxArgs {
     const uint8_t* x;
@@ -46,43 +58,47 @@ struct MxArgs {
 };
 
 // LDS layout.
-//   Data stages (kStages), each the 16 x fragments then the 16 W fragments of one K step. Fragment F
-//   (tile rows 16 F .. 16 F + 15) is 1 KB: row r's four 16-byte K blocks sit at 64 r + 16 (c ^ swz(r)),
-//   so a direct load in which 4 neighbouring lanes read one row's 64 contiguous bytes lands each
-//   chunk where the MFMA operand read (lane 16 j + i takes row i, block j) finds it.
-//   Scale buffers (2), one per 4-step period: 256 x rows of 16 bytes, then 256 W rows; byte 4 t + g
-//   of a row is the scale of group g of step t of the period (the row's 16 scale bytes in memory).
-//   After the K loop the stages hold the output tile on its way to global memory.
-constexpr int kFragBytes = 1024;
-constexpr int kOpBytes = 16 * kFragBytes;
-constexpr int kStageBytes = 2 * kOpBytes;
-constexpr int kStages = 4;
+//   Data regions (2), each two K steps e, e + 1 (e even) of the 256 x rows (32 KB) then the 256 W
+//   rows. Rows come in blocks of 8 (1 KB): step e's 64 bytes of each row in the first 512 bytes,
+//   step e + 1's in the second, row r of the block at 64 (r % 8) + 16 (c ^ swz(r % 16)) for K
+//   block c. A direct load (8 lanes per row: 4 per step half) fills one block, and the swizzle
+//   makes the MFMA operand reads, 16 neighbouring rows per 16 lanes, free of bank conflicts.
+//   Scale buffers (2), one per 4-step period: 256 x rows of 16 bytes, then 256 W rows; byte 4 t + c
+//   of a row is the scale of block c of step t of the period (the row's 16 scale bytes in memory).
+//   After the K loop the regions hold the output tile on its way to global memory.
+constexpr int kGroupBytes = 1024;                            // 8 rows x 2 steps
+constexpr int kOpRegionBytes = 32 * kGroupBytes;             // one operand's 256 rows, two steps
+constexpr int kRegionBytes = 2 * kOpRegionBytes;
 constexpr int kScaleOpBytes = 256 * 16;
 constexpr int kScaleBufBytes = 2 * kScaleOpBytes;
-constexpr int kScaleBase = kStages * kStageBytes;
+constexpr int kScaleBase = 2 * kRegionBytes;
 constexpr int kLdsBytes = kScaleBase + 2 * kScaleBufBytes;   // 144 KB
 constexpr int kPairDma = 16;                                 // direct loads per lane per 2 steps
-constexpr int kScaleDma = 2;                                 // per lane per 4-step period
-constexpr int kOutPitch = 128 + 4;                           // floats per staged output row
+constexpr int kOutPitch = 128 + 8;                           // floats per staged output row
 constexpr int kOutWaveBytes = 32 * kOutPitch * 4;            // 32 rows per wave and pass
 
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 2)) & 3; }
 
-__device__ __forceinline__ i8v operand(uint4 u) {
-    return (i8v){(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
-}
-
-// One wave's operands of one K step: 8 x fragments, 8 W fragments and their scale bytes, one per
-// register in byte 0 (a byte load each, so no ALU op combines them and nothing waits for them
-// before the MFMAs that use them).
+// One wave's operands of one K step: 4 x fragments and 4 W fragments of 32 rows, each as two
+// 64-deep halves, and per fragment the scale bytes of both halves (bytes 0 and 1 of one register,
+// one 16-bit LDS read).
 struct Frags {
-    uint4 a[8], b[8];
-    int sa[8], sb[8];
+    v4u a[4][2], b[4][2];
+    int sa[4], sb[4];
 };
 
-// acc += a . b with the scale bytes of the two fragments (byte 0 of sa and sb: op_sel 0).
-__device__ __forceinline__ f4 mx_mfma(uint4 a, uint4 b, f4 acc, int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(operand(a), operand(b), acc, 4, 4, 0, sa, 0, sb);
+// acc += a . b over one 64-deep half H: v_mfma_scale_f32_32x32x64_f8f6f4 with both operands fp4
+// (cbsz = blgp = 4), the scales in byte H of sa and sb. Lane l holds row (or column) l % 32 and
+// 32 values of the half; the result is column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 for
+// r = 0..15. Written as assembly so that the accumulators stay in place in AGPRs.
+template <int H>
+__device__ __forceinline__ void mx_mfma(f16v& acc, v4u av, v4u bv, int sa, int sb) {
+    if constexpr (H == 0)
+        asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"
+                     : "+a"(acc) : "v"(av), "v"(bv), "v"(sa), "v"(sb));
+    else
+        asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[0,0,0] cbsz:4 blgp:4"
+                     : "+a"(acc) : "v"(av), "v"(bv), "v"(sa), "v"(sb));
 }
 
 // Workgroup barrier after this wave's LDS reads and all but the newest N direct loads have
@@ -111,26 +127,28 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
     const rsrc_t xsr = make_rsrc(a.xs, (uint32_t)M * kg);
     const rsrc_t wsr = make_rsrc(a.ws, (uint32_t)N * kg);
 
-    // Direct loads of wave w: per step, fragments 4 w .. 4 w + 3 of x and of W, lane l reading
-    // row l / 4 of the fragment, chunk (l % 4) ^ swz(row); per period, the 16 scale bytes of rows
-    // 64 w + l. The lane's row offset is loop-invariant in voffset and the step's K offset goes in
-    // soffset; the buffer range check covers their sum, so rows past M or N (offsets from M * K / 2
-    // up, below 2^32 by the launcher's check) load zeros. The scale window of a row may run into the
-    // next row or past the buffer end (K % 512 != 0): those bytes belong to steps past the last
-    // and are never read, and the range check is per dword.
-    const int fr = lane & 15, grp = lane >> 4;
-    const int drow = lane >> 2;
-    const uint32_t dchunk = 16u * (uint32_t)((lane & 3) ^ swz(drow));
-    uint32_t xo[4], wo[4];
+    // Direct loads of wave w: per pair of steps, load q (0..7) covers x (and W) tile rows
+    // 64 w + 8 q .. + 7, lane l reading row 8 q + (l % 32) / 4, step half l / 32, K block
+    // (l % 4) ^ swz(row); per period, the 16 scale bytes of rows 64 w + l. The lane's row offset is
+    // loop-invariant in voffset and the pair's K offset goes in soffset; the buffer range check
+    // covers their sum, so rows past M or N (offsets from M * K / 2 up, below 2^32 by the launcher's
+    // check) load zeros. A step past the last (the second half of a pair when K / 128 is odd) reads
+    // the start of the next row, or zeros, into a half nobody reads. The scale window of a row may
+    // run into the next row or past the buffer end (K % 512 != 0): those bytes belong to steps past
+    // the last and are never read, and the range check is per dword.
+    const int drow = (lane & 31) >> 2;
+    uint32_t xo[8], wo[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        xo[q] = (uint32_t)(m0 + 16 * (4 * wid + q) + drow) * kb + dchunk;
-        wo[q] = (uint32_t)(n0 + 16 * (4 * wid + q) + drow) * kb + dchunk;
+    for (int q = 0; q < 8; ++q) {
+        const int R = 64 * wid + 8 * q + drow;  // tile row
+        const uint32_t c = 16u * (uint32_t)((lane & 3) ^ swz(R & 15)) + 64u * (uint32_t)(lane >> 5);
+        xo[q] = (uint32_t)(m0 + R) * kb + c;
+        wo[q] = (uint32_t)(n0 + R) * kb + c;
     }
     const uint32_t xso = (uint32_t)(m0 + tid) * kg, wso = (uint32_t)(n0 + tid) * kg;
 
     const int nsteps = K / KSTEP;
-    // Steps past the last re-read the last one (cache hits) into a stage nobody reads again.
+    // Pairs past the last re-read the last one (cache hits) into a region nobody reads again.
     // Period p = steps 4 p .. 4 p + 3. A period past the last reads bytes nobody uses into the
     // buffer the last period does not occupy.
     auto dma_scales = [&](int p, uint8_t* buf) {
@@ -138,165 +156,131 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xsr, (lds_void*)(buf + wid * 1024), 16, xso, pofs, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (lds_void*)(buf + kScaleOpBytes + wid * 1024), 16, wso, pofs, 0, 0);
     };
-    // Steps e and e + 1 (e even) are the two 64-byte halves of each row's 128-byte line. They are
-    // loaded as one batch of 16 direct loads, k = 0 .. 15 in issue order [x e][x e + 1][W e][W e + 1]
-    // (4 each), the halves of a row 4 loads apart so that the second request finds the line the
-    // first one brought in.
-    auto dma_batch = [&](int k, int e, uint8_t* st0, uint8_t* st1) {
-        const int op = k >> 3, half = (k >> 2) & 1, q = k & 3;
-        const int kofs = min(e + half, nsteps - 1) * (KSTEP / 2);
+    // Steps e and e + 1 (e even) are the two 64-byte halves of each row's 128-byte line: one direct
+    // load brings 8 whole lines (8 rows), step e to the first 512 bytes of its LDS block and step
+    // e + 1 to the second. A batch is 16 loads, k = 0 .. 15: x rows 64 w + 8 k .., then W rows.
+    auto dma_batch = [&](int k, int e, uint8_t* reg) {
+        const int op = k >> 3, q = k & 7;
+        const int kofs = min(e, nsteps - 1) * (KSTEP / 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            op ? wr : xr, (lds_void*)((half ? st1 : st0) + op * kOpBytes + (4 * wid + q) * kFragBytes), 16,
+            op ? wr : xr, (lds_void*)(reg + op * kOpRegionBytes + (8 * wid + q) * kGroupBytes), 16,
             op ? wo[q] : xo[q], kofs, 0, 0);
     };
-    auto dma_pair = [&](int e, uint8_t* st0, uint8_t* st1) {
+    auto dma_pair = [&](int e, uint8_t* reg) {
 #pragma unroll
-        for (int k = 0; k < kPairDma; ++k) dma_batch(k, e, st0, st1);
+        for (int k = 0; k < kPairDma; ++k) dma_batch(k, e, reg);
     };
 
-    const int rd = 64 * fr + 16 * (grp ^ swz(fr));
-    const int sa_row = 16 * (16 * 8 * wm + fr) + grp;
-    const int sb_row = kScaleOpBytes + 16 * (16 * 8 * wn + fr) + grp;
-    // T = position of the step inside its period (selects the scale byte).
+    // Operand reads. Fragment F of the wave (rows 32 F .. 32 F + 31 of its 128) spans row blocks
+    // 4 F .. 4 F + 3; lane l takes row l % 32 and, for half h, K block 2 (l / 32) + h of the step.
+    // The blocks of a lane's two halves are neighbours, so its two scale bytes are one 16-bit read.
+    const int lq = lane >> 5;
+    int rd[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        rd[h] = kGroupBytes * ((lane & 31) >> 3) + 64 * (lane & 7) + 16 * ((2 * lq + h) ^ swz(lane & 15));
+    const int sa_row = 16 * (128 * wm + (lane & 31)) + 2 * lq;
+    const int sb_row = kScaleOpBytes + 16 * (128 * wn + (lane & 31)) + 2 * lq;
+    auto read_frag = [&](Frags& f, const uint8_t* stage, int op, int F, int h) {
+        if (op == 0)
+            f.a[F][h] = *reinterpret_cast<const v4u*>(stage + (16 * wm + 4 * F) * kGroupBytes + rd[h]);
+        else
+            f.b[F][h] = *reinterpret_cast<const v4u*>(stage + kOpRegionBytes + (16 * wn + 4 * F) * kGroupBytes + rd[h]);
+    };
+    // T = position of the step inside its period (selects the scale bytes).
+    auto read_scale = [&](Frags& f, const uint8_t* sbuf, int T, int op, int F) {
+        if (op == 0)
+            f.sa[F] = *reinterpret_cast<const uint16_t*>(sbuf + sa_row + 512 * F + 4 * T);
+        else
+            f.sb[F] = *reinterpret_cast<const uint16_t*>(sbuf + sb_row + 512 * F + 4 * T);
+    };
     auto lread = [&](Frags& f, const uint8_t* stage, const uint8_t* sbuf, int T) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            f.a[i] = *reinterpret_cast<const uint4*>(stage + (8 * wm + i) * kFragBytes + rd);
-            f.b[i] = *reinterpret_cast<const uint4*>(stage + kOpBytes + (8 * wn + i) * kFragBytes + rd);
-        }
+        for (int k = 0; k < 16; ++k) read_frag(f, stage, k & 1, (k >> 1) & 3, k >> 3);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            f.sa[2 * k] = sbuf[sa_row + 512 * k + 4 * T];
-            f.sa[2 * k + 1] = sbuf[sa_row + 512 * k + 256 + 4 * T];
-            f.sb[2 * k] = sbuf[sb_row + 512 * k + 4 * T];
-            f.sb[2 * k + 1] = sbuf[sb_row + 512 * k + 256 + 4 * T];
-        }
+        for (int k = 0; k < 8; ++k) read_scale(f, sbuf, T, k & 1, k >> 1);
     };
 
-    // quarter 0: W fragments 0-3 and all scales; 1: W 4-7; 2: x 0-3; 3: x 4-7.
-    auto lread_q = [&](Frags& f, const uint8_t* stage, const uint8_t* sbuf, int T, int g) {
-        const int op = g >> 1, i0 = 4 * (g & 1);
+    f16v acc[4][4];
 #pragma unroll
-        for (int i = i0; i < i0 + 4; ++i) {
-            if (op == 0)
-                f.b[i] = *reinterpret_cast<const uint4*>(stage + kOpBytes + (8 * wn + i) * kFragBytes + rd);
-            else
-                f.a[i] = *reinterpret_cast<const uint4*>(stage + (8 * wm + i) * kFragBytes + rd);
-        }
-        if (g == 0) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                f.sa[2 * k] = sbuf[sa_row + 512 * k + 4 * T];
-                f.sa[2 * k + 1] = sbuf[sa_row + 512 * k + 256 + 4 * T];
-                f.sb[2 * k] = sbuf[sb_row + 512 * k + 4 * T];
-                f.sb[2 * k + 1] = sbuf[sb_row + 512 * k + 256 + 4 * T];
-            }
-        }
-    };
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    // The MFMAs below are assembly: the zeroed accumulators must be in their registers, and a few
+    // cycles old, before the first one reads them.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
+    asm volatile("s_nop 7" ::: "memory");
 
-    f4 acc[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-
-    auto stage_at = [&](int s) { return lds + (s & (kStages - 1)) * kStageBytes; };
+    // step s: LDS region (s / 2) % 2, second half of each 1 KB block when s is odd
+    auto region_at = [&](int s) { return lds + ((s >> 1) & 1) * kRegionBytes; };
+    auto stage_at = [&](int s) { return region_at(s) + (s & 1) * 512; };
     auto sbuf_at = [&](int s) { return lds + kScaleBase + ((s >> 2) & 1) * kScaleBufBytes; };
 
-    // Pipeline, at the start of step s: `cur` holds step s's operands and LDS stage (s + 1) % 4 with
-    // the scales of step s + 1 is complete. Step s reads step s + 1's operands into `nxt` while its
-    // MFMAs run. An odd step s also issues the batch of steps s + 3 and s + 4 (stages (s + 3) % 4
-    // and s % 4, read two steps and one step ago), preceded, when s % 4 == 1, by the scales of
-    // period (s + 3) / 4. Every step ends by waiting for the loads the next step reads, the newest
-    // ones staying in flight, and one LDS barrier:
-    //   even s: stage s + 2 = the first half of the last batch; only [W s + 3] may be pending;
-    //   odd s:  stage s + 2 = the second half of the previous batch; this step's batch may be.
+    // Pipeline, at the start of step s: `cur` holds step s's operands and the LDS data of step s + 1
+    // with its scales is complete. Step s reads step s + 1's operands into `nxt` while its MFMAs
+    // run. An odd step s also issues the batch of the pair s + 3, s + 4 into the region of the pair
+    // s - 1, s (read during steps s - 2 and s - 1), and, when s % 4 == 1, the scales of period
+    // (s + 3) / 4 into the buffer period (s - 1) / 4 has left. An even step s ends by waiting for
+    // every load (the batch issued one step before: the pair s + 2, s + 3) and one LDS barrier.
+    // After it, that pair is visible to all waves, and every wave is done with the pair s, s + 1,
+    // whose region the next batch overwrites. Odd steps need no barrier: the step after reads the
+    // second half of a pair already waited for.
     // The pointers given to a step are distinct regions; __restrict__ lets the compiler see that
     // the step's LDS reads cannot alias its direct loads, so it does not wait for them first.
     Frags f0, f1;
-    [&](uint8_t* __restrict__ sc, uint8_t* __restrict__ s0, uint8_t* __restrict__ s1,
-        uint8_t* __restrict__ s2, uint8_t* __restrict__ s3) {
+    [&](uint8_t* __restrict__ sc, uint8_t* __restrict__ s0, uint8_t* r0, uint8_t* r1) {
         dma_scales(0, sc);
-        dma_pair(0, s0, s1);
-        dma_pair(2, s2, s3);
+        dma_pair(0, r0);
+        dma_pair(2, r1);
         stage_barrier<kPairDma>();  // scales and steps 0, 1; steps 2, 3 stay in flight
         lread(f0, s0, sc, 0);
-    }(sbuf_at(0), stage_at(0), stage_at(1), stage_at(2), stage_at(3));
+    }(sbuf_at(0), stage_at(0), region_at(0), region_at(2));
 
-    // P = s % 4 (compile time): odd positions issue a batch, position 1 with scales.
-    auto step = [&](auto Pc, int s, Frags& cur, Frags& nxt, uint8_t* __restrict__ d0,
-                    uint8_t* __restrict__ d1, uint8_t* __restrict__ sdst,
+    // P = s % 4 (compile time): odd positions issue a batch, position 1 with scales. The step's
+    // 32 MFMAs (half 0, then half 1, each over the 4 x 4 fragments) have the other instructions
+    // placed between them: the 16 operand reads after MFMAs 0..15, the 8 scale reads after MFMAs
+    // 16..23, the direct loads after MFMAs 8..23, so that the MFMA pipe is fed while they issue.
+    auto step = [&](auto Pc, int s, Frags& cur, Frags& nxt, uint8_t* __restrict__ dreg,
+                    uint8_t* __restrict__ sdst,
                     const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc) {
         constexpr int P = decltype(Pc)::value;
         constexpr int T1 = (P + 1) & 3;
         constexpr bool batch = P & 1, scales = P == 1;
-        // loads issued after the ones step s + 1 reads: this step's batch and scales
-        constexpr int V = (batch ? kPairDma : 0) + (scales ? kScaleDma : 0);
-        if constexpr (batch) {
-            if (scales) dma_scales((s + 3) >> 2, sdst);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) dma_batch(k, s + 3, d0, d1);
-        }
-        lread_q(nxt, src, ssrc, T1, 0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
+        for (int m = 0; m < 32; ++m) {
+            const int i = (m >> 2) & 3, j = m & 3;
+            if (m < 16)
+                mx_mfma<0>(acc[i][j], cur.a[i][0], cur.b[j][0], cur.sa[i], cur.sb[j]);
+            else
+                mx_mfma<1>(acc[i][j], cur.a[i][1], cur.b[j][1], cur.sa[i], cur.sb[j]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (m < 16) read_frag(nxt, src, m & 1, (m >> 1) & 3, m >> 3);
+            if (m >= 16 && m < 24) read_scale(nxt, ssrc, T1, m & 1, (m - 16) >> 1);
+            if constexpr (batch) {
+                if (scales && m == 24) dma_scales((s + 3) >> 2, sdst);
+                if (m >= 8 && m < 24) dma_batch(m - 8, s + 3, dreg);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (batch) {
+        // The MFMAs above read their operands as they issue, but the compiler sees assembly: keep
+        // every operand register of this step out of reach of the reads into `nxt` until here.
 #pragma unroll
-            for (int k = 4; k < 8; ++k) dma_batch(k, s + 3, d0, d1);
-        }
-        lread_q(nxt, src, ssrc, T1, 1);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 2; i < 4; ++i) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (batch) {
-#pragma unroll
-            for (int k = 8; k < 12; ++k) dma_batch(k, s + 3, d0, d1);
-        }
-        lread_q(nxt, src, ssrc, T1, 2);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 4; i < 6; ++i) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (batch) {
-#pragma unroll
-            for (int k = 12; k < 16; ++k) dma_batch(k, s + 3, d0, d1);
-        }
-        lread_q(nxt, src, ssrc, T1, 3);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 6; i < 8; ++i) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[i][j] = mx_mfma(cur.a[i], cur.b[j], acc[i][j], cur.sa[i], cur.sb[j]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        stage_barrier<batch ? V : kPairDma / 4>();
+        for (int i = 0; i < 4; ++i)
+            asm volatile("" ::"v"(cur.a[i][0]), "v"(cur.a[i][1]), "v"(cur.b[i][0]), "v"(cur.b[i][1]),
+                         "v"(cur.sa[i]), "v"(cur.sb[i]));
+        if constexpr (!batch) stage_barrier<0>();
         __builtin_amdgcn_sched_barrier(0);
     };
-    // d0 / d1 (stages (s + 3) % 4 and s % 4) and sdst (the buffer of period (s + 3) / 4, which
+    // dreg (the region of the pair s + 3, s + 4) and sdst (the buffer of period (s + 3) / 4, which
     // step s + 1 does not read) are only written by odd steps.
 #define MX_STEP(P, S, CUR, NXT)                                                                   \
-    step(std::integral_constant<int, P>{}, S, CUR, NXT, stage_at((S) + 3), stage_at((S) + 4),       \
-         sbuf_at((S) + 3), stage_at((S) + 1), sbuf_at((S) + 1))
+    step(std::integral_constant<int, P>{}, S, CUR, NXT, region_at((S) + 3), sbuf_at((S) + 3),     \
+         stage_at((S) + 1), sbuf_at((S) + 1))
     int s = 0;
     for (; s + 3 < nsteps; s += 4) {
         MX_STEP(0, s, f0, f1);
@@ -308,10 +292,17 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
     if (s + 1 < nsteps) MX_STEP(1, s + 1, f1, f0);
     if (s + 2 < nsteps) MX_STEP(2, s + 2, f0, f1);
 #undef MX_STEP
+    // The compiler does not see the MFMAs' results arrive late: wait out the longest MFMA latency
+    // before the accumulators are read.
+    asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
     stage_barrier<0>();  // every direct load has landed and every wave is done with the stages
 
-    // Output: per wave, 4 passes of 32 rows (fragment rows 2 p, 2 p + 1) staged as fp32 in the
-    // wave's own LDS region, then written back a full row segment per lane group: 16-byte stores.
+    // Output: per wave, 4 passes of 32 rows (fragment row F = p) staged as fp32 in the wave's own
+    // LDS region, then written back a full row segment per lane group: 16-byte stores.
     float* ostage = reinterpret_cast<float*>(lds + wid * kOutWaveBytes);
     const int ro = m0 + wm * 128, co = n0 + wn * 128;
     constexpr int es = YT == BYHIP_F32 ? 4 : 2;
@@ -319,12 +310,10 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    ostage[(16 * ii + 4 * grp + r) * kOutPitch + 16 * j + fr] = acc[2 * p + ii][j][r];
+            for (int r = 0; r < 16; ++r)
+                ostage[(8 * (r >> 2) + 4 * lq + (r & 3)) * kOutPitch + 32 * j + (lane & 31)] = acc[p][j][r];
         __builtin_amdgcn_wave_barrier();
         // 16 output bytes per lane: 4 floats (f32) or 8 halves.
         constexpr int per = 16 / es;                 // elements per lane
@@ -383,8 +372,9 @@ void launch_mxfp4(const uint8_t* x, const uint8_t* x_scales, const uint8_t* w,
                   const uint8_t* w_scales, void* y, int y_dtype, int M, int K, int N) {
     if (K % KSTEP != 0) fail("byhip: internal: MXFP4 GEMM needs K %% 128 == 0 (K=%d)", K);
     if (M <= 0 || N <= 0) return;
-    // Buffer offsets of the rows a tile reaches past M or N must stay below 2^32.
-    if ((uint64_t)(M + TM) * (K / 2) >= kOutOfRange || (uint64_t)(N + TN) * (K / 2) >= kOutOfRange)
+    // Buffer offsets of the rows a tile reaches past M or N (plus the second half of a last pair
+    // of steps) must stay below 2^32.
+    if ((uint64_t)(M + TM) * (K / 2) + 128 >= kOutOfRange || (uint64_t)(N + TN) * (K / 2) + 128 >= kOutOfRange)
         fail("byhip: MXFP4 operands above 4 GiB are not supported");
     MxArgs a;
     a.x = x; a.xs = x_scales; a.w = w; a.ws = w_scales; a.y = y;
