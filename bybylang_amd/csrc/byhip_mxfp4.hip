@@ -341,15 +341,13 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
                     uint32_t w[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        uint32_t lo, hi;
                         if constexpr (YT == BYHIP_F16) {
-                            lo = __builtin_bit_cast(uint16_t, (_Float16)v[2 * e]);
-                            hi = __builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]);
+                            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)v[2 * e]);
+                            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]);
+                            w[e] = lo | (hi << 16);
                         } else {
-                            lo = f32_to_bf16_bits(v[2 * e]);
-                            hi = f32_to_bf16_bits(v[2 * e + 1]);
+                            w[e] = f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]);
                         }
-                        w[e] = lo | (hi << 16);
                     }
                     o = make_uint4(w[0], w[1], w[2], w[3]);
                 }
