@@ -168,6 +168,37 @@ def test_mxfp4_gemm_against_oracle(hip, oracle, shape, yt):
     tier_check(y2.read(np.float32), want, TIER_F32_ACC)
 
 
+@pytest.mark.parametrize("shape", [(300, 640, 520), (70, 768, 260), (257, 896, 300), (40, 1152, 600),
+                                   (520, 1536, 130)])
+def test_mxfp4_gemm_pipeline_tails(hip, oracle, shape):
+    """K steps (128 deep) of 5, 6, 7, 9 and 12: the step loop runs in groups of four with one to three
+    steps after it, and loads come in pairs of steps, so odd counts end on half a pair. M and N are
+    not multiples of the 256 x 256 tile. fp32 output against the oracle at 1e-5 (exact products)."""
+    M, K, N = shape
+    xb, xdec, wb, table = mx_case(M, K, N, 11 * M + N)
+    want = oracle.tile_gemm(0, M, K, N, N * (K // 2), 0, wb, table, xdec.reshape(-1))
+    y = hip.DeviceBuffer(M * N * 4)
+    print(f"mxfp4 tails {shape}", flush=True)
+    hip.mxfp4_gemm(hip.DeviceBuffer.from_array(xb), hip.DeviceBuffer.from_array(wb), y, hip.F32, M, K, N)
+    got = y.read(np.float32)
+    assert np.isfinite(got).all()
+    assert max_abs_rel(got, want) < 1e-5
+
+
+def test_mxfp4_bf16_output_is_rne_of_f32(hip):
+    """The bf16 output is the fp32 result rounded to nearest even, bit for bit: both come from the
+    same accumulators, so this pins the hardware conversion on the GEMM's own values."""
+    M, K, N = 256, 1024, 512
+    xb, _, wb, _ = mx_case(M, K, N, 5)
+    x, w = hip.DeviceBuffer.from_array(xb), hip.DeviceBuffer.from_array(wb)
+    y32, y16 = hip.DeviceBuffer(M * N * 4), hip.DeviceBuffer(M * N * 2)
+    hip.mxfp4_gemm(x, w, y32, hip.F32, M, K, N)
+    hip.mxfp4_gemm(x, w, y16, hip.BF16, M, K, N)
+    f = y32.read(np.float32)
+    want = (f32_to_bf16_rne(f).view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(y16.read(np.uint16), want)
+
+
 def test_mxfp4_route_refuses_other_tables(hip):
     M, K, N = 16, 128, 32
     xb, _, wb, table = mx_case(M, K, N, 1)
