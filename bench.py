@@ -56,9 +56,13 @@ def mx_bytes(M, K, N):
 class Recorder:
     """Records `fn(step)` for `count` steps as one session recording (a HIP graph)."""
 
-    def __init__(self, fn, count):
+    @staticmethod
+    def gb_module():
         from bybylang_amd import gpubackend as gb
-        self.gb = gb
+        return gb
+
+    def __init__(self, fn, count):
+        gb = self.gb = self.gb_module()
         assert gb.sessionBeginRecording(gb.gbHip), gb.sessionGetLastError(gb.gbHip)
         for i in range(count):
             fn(i)
@@ -79,17 +83,60 @@ class Recorder:
         self.gb.sessionFreeRecording(self.gb.gbHip, self.id)
 
 
-def run_steps(fn, steps, warmup):
-    """Warmup recording replayed once, then the timed recording of exactly `steps` steps."""
-    if warmup > 0:
-        w = Recorder(fn, warmup)
-        w.timed()
-        w.close()
-    r = Recorder(fn, steps)
+SETTLE_MS = 100.0  # GPU time of untimed work before each timing, so the clocks are out of idle
+# The timing marks are the library's events recorded inside the recording, around exactly the
+# timed steps (byhip_session_mark); without them (BENCH_MARKS=0) the lead-in and the timed steps are
+# two recordings queued back to back with events between them (byhip_session_replay_after).
+MARKS_IN_RECORDING = os.environ.get("BENCH_MARKS", "1") != "0"
+
+
+def run_steps(fn, steps, warmup, settle_steps=8):
+    """Returns (GPU seconds of exactly `steps` timed steps, wall seconds of that replay).
+
+    Step indices are global and every rotation continues across the phases: the settle recording
+    is fn(-settle_steps .. -1), the warmup fn(0 .. W-1), the timed run fn(W .. W+S-1). Recordings
+    run once when they are made; the settle recording (one full weight rotation where the caller
+    rotates copies) is then replayed until SETTLE_MS of GPU time has passed, which also leaves
+    every copy's last read in rotation order. Finally the lead-in recording (the settle rotation,
+    then the W warmup steps) and the timed recording are queued back to back and only the latter
+    is timed: the lead-in lasts long enough for the host to queue the timed launch behind it, so
+    the GPU never waits for the host inside the timed region, and the first timed step reads a copy
+    last read a whole rotation earlier."""
+    from bybylang_amd import _abi
+    gb = Recorder.gb_module()
+    lib = _abi.load()
+    settle = Recorder(lambda i: fn(i - settle_steps), settle_steps)
+    marked = MARKS_IN_RECORDING
+
+    def whole(i):
+        # lead-in and timed steps in one recording, the timing marks between them
+        if marked and i == settle_steps + warmup:
+            _abi.check(lib.byhip_session_mark(0), "mark")
+        fn(i - settle_steps)
+        if marked and i == settle_steps + warmup + steps - 1:
+            _abi.check(lib.byhip_session_mark(1), "mark")
+
+    if marked:
+        run = Recorder(whole, settle_steps + warmup + steps)
+        recs = (settle, run)
+    else:
+        lead = Recorder(lambda i: fn(i - settle_steps), settle_steps + warmup)
+        timed = Recorder(lambda i: fn(i + warmup), steps)
+        recs = (settle, lead, timed)
+    spent = 0.0
+    while spent < SETTLE_MS * 1e-3:
+        spent += settle.timed()
+    assert gb.sessionSetGpuTiming(gb.gbHip, True)
     wall0 = time.perf_counter()
-    gpu_s = r.timed()
+    if marked:
+        _abi.check(lib.byhip_session_replay_marked(run.id), "replay")
+    else:
+        _abi.check(lib.byhip_session_replay_after(lead.id, 1, timed.id, 1), "replay")
     wall = time.perf_counter() - wall0
-    r.close()
+    gpu_s = gb.sessionGpuSeconds(gb.gbHip)
+    gb.sessionSetGpuTiming(gb.gbHip, False)
+    for r in recs:
+        r.close()
     return gpu_s, wall
 
 
@@ -108,7 +155,7 @@ def bench_c1(dev, synth, steps, warmup):
     copies = max(1, -(-ROTATE_BYTES // nbytes))
     ws, x, y = q4_setup(dev, synth, 1, M, K, N, copies)
     fn = lambda i: dev.q4_matmul(x, dev.F16, ws[i % copies], y, dev.F16, M)  # noqa: E731
-    gpu_s, wall = run_steps(fn, steps, warmup)
+    gpu_s, wall = run_steps(fn, steps, warmup, settle_steps=copies)
     per = gpu_s / steps
     res = {"M": M, "K": K, "N": N, "bytes_per_step": nbytes, "weight_copies": copies,
            "rotation_bytes": nbytes * copies, "us_per_step": per * 1e6,
@@ -167,7 +214,7 @@ def bench_c4(dev, synth, steps, warmup, tuned=False):
         per_op = {}
         for j, (name, K, N) in enumerate(C4_OPS):
             fn = lambda i, j=j: dev.q4_matmul(xs[j], dev.F16, weights[j][i % copies], ys[j], dev.F16, M)  # noqa: E731
-            gpu_s, _ = run_steps(fn, steps, warmup)
+            gpu_s, _ = run_steps(fn, steps, warmup, settle_steps=copies)
             per = gpu_s / steps
             b, f = q4_bytes(M, K, N), 2 * M * K * N
             per_op[name] = {"us": per * 1e6, "GBps": b / per / 1e9, "TFLOPs": f / per / 1e12}
@@ -176,7 +223,7 @@ def bench_c4(dev, synth, steps, warmup, tuned=False):
             for j in range(len(C4_OPS)):
                 dev.q4_matmul(xs[j], dev.F16, weights[j][i % copies], ys[j], dev.F16, M)
 
-        gpu_s, _ = run_steps(layer, steps, warmup)
+        gpu_s, _ = run_steps(layer, steps, warmup, settle_steps=copies)
         per = gpu_s / steps
         flops = sum(2 * M * K * N for _, K, N in C4_OPS)
         out[f"M{M}"] = {"per_op": per_op, "batch_us": per * 1e6,
@@ -193,7 +240,7 @@ def bench_c4(dev, synth, steps, warmup, tuned=False):
                         dev.q4_prepare(w, M, dev.F16)
                     info = dev.q4_plan_info(weights[j][0], M, dev.F16)
                     plans[name] = info[0] if info else None
-                gpu_s, _ = run_steps(layer, steps, warmup)
+                gpu_s, _ = run_steps(layer, steps, warmup, settle_steps=copies)
                 per = gpu_s / steps
                 out[f"M{M}"]["tuned"] = {"batch_us": per * 1e6, "plans": plans}
                 dev.q4_plans_reset()
@@ -279,7 +326,7 @@ def bench_c4_fused(dev, synth, steps, warmup):
     out = {"per_op": {}}
     for op in ops:
         name, mode, K, Ns, norm, res = op[:6]
-        gpu_s, _ = run_steps(lambda i, op=op: call(op, i), steps, warmup)
+        gpu_s, _ = run_steps(lambda i, op=op: call(op, i), steps, warmup, settle_steps=copies)
         per = gpu_s / steps
         out["per_op"][name] = {"us": per * 1e6, "GBps": fused_bytes(mode, K, Ns, norm, res) / per / 1e9}
 
@@ -287,7 +334,7 @@ def bench_c4_fused(dev, synth, steps, warmup):
         for op in ops:
             call(op, i)
 
-    gpu_s, _ = run_steps(layer, steps, warmup)
+    gpu_s, _ = run_steps(layer, steps, warmup, settle_steps=copies)
     per = gpu_s / steps
     out.update({"batch_us": per * 1e6, "batch_GBps": layer_bytes / per / 1e9, "weight_copies": copies,
                 "launches": len(C4_FUSED)})
@@ -420,8 +467,7 @@ def main() -> int:
     if "c3" in wanted:
         configs["c3_mxfp4_gemm"] = bench_c3(dev, synth, args.steps, args.warmup)
     if "c4" in wanted or "c4t" in wanted:
-        configs["c4_layer_batch"] = bench_c4(dev, synth, max(1, args.steps // 5), max(0, args.warmup // 5),
-                                             tuned="c4t" in wanted)
+        configs["c4_layer_batch"] = bench_c4(dev, synth, args.steps, args.warmup, tuned="c4t" in wanted)
     if "up" in wanted:
         configs["resident_upload_mapped"] = bench_upload_mapped(synth)
     if "rp" in wanted:

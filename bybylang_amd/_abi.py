@@ -37,7 +37,7 @@ class Q4WInfo(C.Structure):
     _fields_ = [("K", C.c_int), ("N", C.c_int), ("group_size", C.c_int),
                 ("groups_per_row", C.c_int), ("scale_is_f16", C.c_int),
                 ("zero_uniform", C.c_int), ("zero_value", C.c_float),
-                ("device_bytes", C.c_size_t)]
+                ("device_bytes", C.c_size_t), ("f16_safe", C.c_int)]
 
 
 _VP, _SZ, _I, _U8P, _FP = C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p
@@ -72,6 +72,9 @@ SIGNATURES = {
     "byhip_session_begin_recording": (_I, []),
     "byhip_session_last_recording": (_I, []),
     "byhip_session_replay": (_I, [_I, _I]),
+    "byhip_session_replay_after": (_I, [_I, _I, _I, _I]),
+    "byhip_session_mark": (_I, [_I]),
+    "byhip_session_replay_marked": (_I, [_I]),
     "byhip_session_free_recording": (_I, [_I]),
     "byhip_q4_resident_upload": (_I, [_U8P, _SZ, _SZ, _FP, _FP, _I, _I, _I, _I, C.POINTER(_VP)]),
     "byhip_q4_resident_from_device": (_I, [_VP, _SZ, _VP, _VP, _I, _I, _I, _I, C.POINTER(_VP)]),

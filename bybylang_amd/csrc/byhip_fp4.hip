@@ -6,8 +6,10 @@
 // [N, K/32] at scale_base. fp32/fp16 activations take the fp16 MFMA GEMM with the weights decoded
 // through the table in LDS; activations already in MXFP4 take the scaled MFMA when the table is
 // exactly E2M1 and 2^(e-127).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "byhip_gemm.h"
 #include "byhip_internal.h"
@@ -15,7 +17,7 @@
 
 namespace byhip {
 
-void q4_matmul_run(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
+void q4_matmul_run(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, bool exact);
 
 namespace {
 
@@ -52,6 +54,30 @@ __global__ void fp4km_unpack(const uint8_t* __restrict__ blob, size_t scale_base
 
 }  // namespace
 
+// Whether every product lut[i] * lut[16 + b] (i < 16, b < 256), formed in fp32 as the reference
+// forms it, is a finite fp16 value: then the fp16 MFMA kernel holds every weight exactly. The last
+// table classified is remembered (a model keeps one table).
+bool table_products_are_halves(const float* t) {
+    static std::mutex mu;
+    static float last[272];
+    static bool have = false, last_ok = false;
+    std::lock_guard<std::mutex> lk(mu);
+    if (have && memcmp(last, t, sizeof last) == 0) return last_ok;
+    bool ok = true;
+    for (int b = 0; b < 256 && ok; ++b)
+        for (int i = 0; i < 16; ++i) {
+            const float p = t[i] * t[16 + b];
+            if (!std::isfinite(p) || (float)(_Float16)p != p) {
+                ok = false;
+                break;
+            }
+        }
+    memcpy(last, t, sizeof last);
+    have = true;
+    last_ok = ok;
+    return ok;
+}
+
 void fp4km_run(const void* x, int x_dtype, const uint8_t* blob, size_t blob_bytes, size_t scale_base,
                const float* lut, size_t lut_floats, size_t lut_base, void* y, int y_dtype, int M,
                int K, int N) {
@@ -79,12 +105,21 @@ void fp4km_run(const void* x, int x_dtype, const uint8_t* blob, size_t blob_byte
     }
     if (x_dtype != BYHIP_F32 && x_dtype != BYHIP_F16) fail("byhip: tile GEMM activations must be F32, F16 or MXFP4_KM");
     check_span(x, (size_t)M * K * dtype_bytes(x_dtype), "tile GEMM activations");
-    if (reinterpret_cast<uintptr_t>(blob) % 16 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0)
-        unsupported("byhip: tile GEMM needs 16-byte aligned weights and activations");
     GemmArgs a;
     a.x = x; a.x_dtype = x_dtype; a.y = y; a.y_dtype = y_dtype; a.M = M; a.K = K; a.N = N;
     a.blob = blob; a.scale_base = scale_base; a.lut = lut + lut_base;
-    launch_gemm(BFormat::Fp4Km, a);
+    // The fp16 MFMA kernel when every decoded weight is a half (the table is read from its host
+    // copy, or from the device outside a recording); otherwise the exact fp32 GEMM.
+    float t[272];
+    const bool aligned = reinterpret_cast<uintptr_t>(blob) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (aligned && env_int("BYHIP_TILE_EXACT", 0) == 0 && try_read_small(lut, lut_base * 4, t, sizeof t) &&
+        table_products_are_halves(t)) {
+        launch_gemm(BFormat::Fp4Km, a);
+        return;
+    }
+    if (reinterpret_cast<uintptr_t>(blob) % 16 != 0)
+        unsupported("byhip: tile GEMM needs 16-byte aligned weights");
+    launch_gemm_exact(BFormat::Fp4Km, a);
 }
 
 void f16_run(const void* x, int x_dtype, const uint16_t* w, size_t w_halves, void* y, int y_dtype,
@@ -97,12 +132,15 @@ void f16_run(const void* x, int x_dtype, const uint16_t* w, size_t w_halves, voi
     check_span(w, (size_t)N * K * 2, "FP16 weights");
     check_span(x, (size_t)M * K * dtype_bytes(x_dtype), "tile GEMM activations");
     check_span(y, (size_t)M * N * dtype_bytes(y_dtype), "tile GEMM output");
-    if (reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0)
-        unsupported("byhip: FP16 tile GEMM needs 16-byte aligned weights and activations");
     GemmArgs a;
     a.x = x; a.x_dtype = x_dtype; a.y = y; a.y_dtype = y_dtype; a.M = M; a.K = K; a.N = N;
     a.w16 = w;
-    launch_gemm(BFormat::F16, a);
+    // Halves are exact in the fp16 MFMA kernel (fp32 activations as two fp16 terms); it reads
+    // 16-byte words, so unaligned operands take the exact kernel, which reads element by element.
+    if (reinterpret_cast<uintptr_t>(w) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
+        launch_gemm(BFormat::F16, a);
+    else
+        launch_gemm_exact(BFormat::F16, a);
 }
 
 }  // namespace byhip
@@ -245,70 +283,122 @@ int byhip_program_dispatch(const uint32_t* words, int n_words, void* mem, size_t
                            const void* input, size_t input_len, int rows) {
     return guard([&] {
         enter_compute();
-        if (!words || n_words <= 0 || !mem || mem_len == 0) fail("byhip: invalid program arguments");
+        // The reference's checks in its order (cpu_vm.c:178-188, 420-628), with its messages.
+        if (!words || n_words <= 0 || !mem || mem_len == 0) fail("invalid CPU VM arguments");
         const uint32_t w0 = words[0], op = w0 & 0xFFu, fmt = reg_a(w0);
         if (op != 0xB0 && op != 0xAC && op != 0xAA && op != 0xAB)
             unsupported("byhip: program op 0x%02x is not a tile GEMM / Q4 / FP4 shape op", op);
         if (n_words < 6)
-            fail(op == 0xB0 ? "byhip: truncated tile GEMM header"
-                            : (op == 0xAC ? "byhip: truncated FP4 shape op" : "byhip: truncated Q4 shape op"));
+            fail(op == 0xB0 ? "CPU VM truncated tile GEMM header"
+                            : (op == 0xAC ? "CPU VM truncated FP4 shape op" : "CPU VM truncated Q4 shape op"));
+        uint32_t M = words[1];
+        const uint32_t K = words[2], N = words[3];
+        const float* in = static_cast<const float*>(input ? input : mem);
+        const size_t in_len = input ? input_len : mem_len;
+
+        // Shape and slot validation; then `stop`, the first output (row-major) at which the
+        // reference stops with `msg` (it checks each output's inputs before storing it), or -1.
+        int64_t stop = -1;
+        char msg[160] = "";
+        auto stop_at = [&](int64_t at, const char* text) {
+            if (stop < 0 || at < stop) {
+                stop = at;
+                snprintf(msg, sizeof msg, "%s", text);
+            }
+        };
+        auto store_stop = [&](const char* what) {
+            if ((uint64_t)M * N > mem_len) {
+                char t[96];
+                snprintf(t, sizeof t, "CPU VM %s out of range: %lld", what, (long long)mem_len);
+                if (stop < 0 || (int64_t)mem_len < stop) stop_at((int64_t)mem_len, t);
+            }
+        };
+        const uint32_t group = words[4], n_groups = words[5];
+        if (op == 0xB0) {
+            if (fmt > 1u || !K || K % 32u || !N)
+                fail("CPU VM unsupported tile GEMM (format %u K %u N %u)", fmt, K, N);
+            if (!u8 || (fmt == 0u && !lut)) fail("CPU VM tile GEMM slot is missing");
+            if (M == 0) M = rows > 0 ? (uint32_t)rows : (uint32_t)(in_len / K);
+            const bool range = fmt == 1u ? (uint64_t)N * K * 2 > u8_len
+                                         : ((uint64_t)N * (K / 2) > u8_len || (uint64_t)words[4] + (uint64_t)N * (K / 32) > u8_len ||
+                                            (uint64_t)words[5] + 272 > lut_len);
+            if (range || (uint64_t)M * K > in_len) fail("CPU VM tile GEMM input out of range");
+            store_stop("tile_gemm_store");
+        } else if (op == 0xAC) {
+            if (!M || !K || K % 64u || N < 16u || group != 32u || n_groups != K / 32u)
+                fail("CPU VM unsupported FP4 cooperative shape");
+            if (!u8 || !lut) fail("CPU VM FP4 cooperative slot is missing");
+            const uint64_t scale_bytes = (uint64_t)N * (K / 2);
+            const uint64_t lut_base = (scale_bytes + (uint64_t)N * n_groups + 3u) / 4u;
+            if (scale_bytes + (uint64_t)N * n_groups > u8_len || lut_base + 272 > lut_len || (uint64_t)M * K > in_len)
+                fail("CPU VM FP4 cooperative input out of range");
+            store_stop("fp4_coop_store");
+        } else {
+            const bool coop = op == 0xAA;
+            if (!M || !N || !K || !group || K % group || n_groups != K / group ||
+                (coop && (N < 16u || K % 64u || group % 2u)) || (!coop && (K % 8u || group % 8u)))
+                fail(coop ? "CPU VM unsupported Q4 cooperative shape" : "CPU VM unsupported Q4 GEMV shape");
+            if (!u8 || !lut) fail("CPU VM Q4 cooperative slot is missing");
+            // Output (r, c) reads bytes c * K/2 + k/2, zeros at zero_base + c * groups + k / group
+            // (past every scale it reads) and x[r * K + k]: its largest indices decide it.
+            const uint64_t rb = K / 2u, scale_base = ((uint64_t)N * rb + 3u) / 4u;
+            const uint64_t zero_base = scale_base + (uint64_t)N * n_groups;
+            auto first_col = [](uint64_t at0, uint64_t per_col, uint64_t len) {
+                return at0 >= len ? (uint64_t)0 : (len - at0 + per_col - 1) / per_col;
+            };
+            const uint64_t c_in = std::min(first_col((K - 1u) / 2u, rb, u8_len),
+                                           first_col(zero_base + (K - 1u) / group, n_groups, lut_len));
+            const uint64_t r_x = in_len / K;  // the first row whose activations run past the input
+            int64_t in_stop = -1;
+            if (r_x == 0 || c_in == 0) in_stop = 0;
+            else if (c_in < N) in_stop = (int64_t)c_in;
+            else if (r_x < M) in_stop = (int64_t)(r_x * N);
+            if (in_stop >= 0) stop_at(in_stop, "CPU VM Q4 cooperative input out of range");
+            store_stop("q4_coop_store");
+        }
         for (int pc = 6; pc < n_words; ++pc) {
             const uint32_t o = words[pc] & 0xFFu;
             if (o == 0x01) break;
             if (!tile_op_noop(o)) unsupported("byhip: op 0x%02x after a shape op has no HIP route", o);
         }
-        uint32_t M = words[1];
-        const uint32_t K = words[2], N = words[3];
-        const float* in = static_cast<const float*>(input ? input : mem);
-        const size_t in_len = input ? input_len : mem_len;
-        if (op == 0xB0) {
-            if (fmt > 1u || !K || K % 32u || !N)
-                fail("byhip: unsupported tile GEMM (format %u K %u N %u)", fmt, K, N);
-            if (M == 0) M = rows > 0 ? (uint32_t)rows : (uint32_t)(in_len / K);
-            if (M == 0) return;
-            if ((size_t)M * K > in_len || (size_t)M * N > mem_len) fail("byhip: tile GEMM input out of range");
-            if (fmt == 1u) {
-                if ((size_t)N * K * 2 > u8_len) fail("byhip: tile GEMM input out of range");
-                f16_run(in, BYHIP_F32, static_cast<const uint16_t*>(u8), u8_len / 2, mem, BYHIP_F32, M, K, N);
+
+        // The outputs the reference computes before it stops (all of them when it does not):
+        // whole rows, then the first columns of the next row.
+        const uint64_t total = (uint64_t)M * N, done = stop < 0 ? total : std::min<uint64_t>((uint64_t)stop, total);
+        auto run = [&](uint32_t Mx, uint32_t Nx, const float* xp, float* yp) {
+            if (!Mx || !Nx) return;
+            if (op == 0xB0 && fmt == 1u) {
+                f16_run(xp, BYHIP_F32, static_cast<const uint16_t*>(u8), u8_len / 2, yp, BYHIP_F32, Mx, K, Nx);
+            } else if (op == 0xB0) {
+                fp4km_run(xp, BYHIP_F32, static_cast<const uint8_t*>(u8), u8_len, words[4],
+                          static_cast<const float*>(lut), lut_len, words[5], yp, BYHIP_F32, Mx, K, Nx);
+            } else if (op == 0xAC) {
+                const size_t scale_bytes = (size_t)N * (K / 2);
+                const size_t lut_base = (scale_bytes + (size_t)N * n_groups + 3u) / 4u;
+                fp4km_run(xp, BYHIP_F32, static_cast<const uint8_t*>(u8), u8_len, scale_bytes,
+                          static_cast<const float*>(lut), lut_len, lut_base, yp, BYHIP_F32, Mx, K, Nx);
             } else {
-                fp4km_run(in, BYHIP_F32, static_cast<const uint8_t*>(u8), u8_len, words[4],
-                          static_cast<const float*>(lut), lut_len, words[5], mem, BYHIP_F32, M, K, N);
+                // The Q4 shape ops are fp32 arithmetic in the reference: the exact routes.
+                const size_t rb = K / 2u, scale_base = ((size_t)N * rb + 3u) / 4u;
+                const size_t zero_base = scale_base + (size_t)N * n_groups;
+                check_span(u8, (size_t)Nx * rb, "Q4 nibbles");
+                check_span(static_cast<const float*>(lut) + scale_base, ((size_t)N * n_groups + (size_t)Nx * n_groups) * 4,
+                           "Q4 scales and zeros");
+                byhip_q4w w{};
+                w.K = (int)K; w.N = (int)Nx; w.group = (int)group; w.gpr = (int)n_groups; w.row_bytes = rb;
+                w.wq = const_cast<uint8_t*>(static_cast<const uint8_t*>(u8));
+                w.scales = const_cast<float*>(static_cast<const float*>(lut) + scale_base);
+                w.zeros = const_cast<float*>(static_cast<const float*>(lut) + zero_base);
+                w.scale_f16 = 0;
+                w.zero_uniform = 0;
+                q4_matmul_run(xp, BYHIP_F32, &w, yp, BYHIP_F32, (int)Mx, true);
             }
-            return;
-        }
-        const uint32_t group = words[4], n_groups = words[5];
-        if (op == 0xAC) {
-            if (!M || !K || K % 64u || N < 16u || group != 32u || n_groups != K / 32u)
-                fail("byhip: unsupported FP4 cooperative shape");
-            const size_t scale_bytes = (size_t)N * (K / 2);
-            const size_t lut_base = (scale_bytes + (size_t)N * n_groups + 3u) / 4u;
-            if (scale_bytes + (size_t)N * n_groups > u8_len || lut_base + 272 > lut_len ||
-                (size_t)M * K > in_len || (size_t)M * N > mem_len)
-                fail("byhip: FP4 cooperative input out of range");
-            fp4km_run(in, BYHIP_F32, static_cast<const uint8_t*>(u8), u8_len, scale_bytes,
-                      static_cast<const float*>(lut), lut_len, lut_base, mem, BYHIP_F32, M, K, N);
-            return;
-        }
-        const bool coop = op == 0xAA;
-        if (!M || !N || !K || !group || K % group || n_groups != K / group ||
-            (coop && (N < 16u || K % 64u || group % 2u)) || (!coop && (K % 8u || group % 8u)))
-            fail(coop ? "byhip: unsupported Q4 cooperative shape" : "byhip: unsupported Q4 GEMV shape");
-        const size_t row_bytes = K / 2u;
-        const size_t scale_base = ((size_t)N * row_bytes + 3u) / 4u;
-        const size_t zero_base = scale_base + (size_t)N * n_groups;
-        if ((size_t)N * row_bytes > u8_len || zero_base + (size_t)N * n_groups > lut_len ||
-            (size_t)M * K > in_len || (size_t)M * N > mem_len)
-            fail("byhip: Q4 cooperative input out of range");
-        check_span(u8, (size_t)N * row_bytes, "Q4 nibbles");
-        check_span(static_cast<const float*>(lut) + scale_base, (size_t)N * n_groups * 8, "Q4 scales and zeros");
-        byhip_q4w w{};
-        w.K = (int)K; w.N = (int)N; w.group = (int)group; w.gpr = (int)n_groups; w.row_bytes = row_bytes;
-        w.wq = const_cast<uint8_t*>(static_cast<const uint8_t*>(u8));
-        w.scales = const_cast<float*>(static_cast<const float*>(lut) + scale_base);
-        w.zeros = const_cast<float*>(static_cast<const float*>(lut) + zero_base);
-        w.scale_f16 = 0;
-        w.zero_uniform = 0;
-        q4_matmul_run(in, BYHIP_F32, &w, mem, BYHIP_F32, (int)M);
+        };
+        float* y = static_cast<float*>(mem);
+        const uint32_t full = (uint32_t)(done / N), rem = (uint32_t)(done % N);
+        run(full, N, in, y);
+        run(rem ? 1u : 0u, rem, in + (size_t)full * K, y + (size_t)full * N);
+        if (stop >= 0) fail("%s", msg);
     });
 }
 

@@ -1,6 +1,8 @@
 // byhip_gemm.h - host-side launchers of the MFMA GEMM kernels (internal to libbybyhip.so).
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include <cstddef>
 #include <cstdint>
 
@@ -41,10 +43,36 @@ struct GemmArgs {
     // writes fp32 partial sums to part[z][M][N]; a second kernel adds them in z order into y.
     float* part = nullptr;
     int split_steps = 0;
+    // Device scratch the launches may use (split-K partials, per-row activation exponents), in
+    // stream order: null means the library workspace (kWorkspaceBytes, allocated at init).
+    void* work = nullptr;
+    size_t work_bytes = 0;
+    // Set by the fp32-activation launch of the fp16 MFMA kernel: per-row exponents t (x * 2^t is
+    // split into fp16 hi + lo; the row's sums are scaled by 2^-t).
+    const int* row_shift = nullptr;
 };
 
-// Queues the GEMM on the library stream; K % 32 == 0 is required (callers check).
+// Floats between consecutive split-K partials (16-byte aligned).
+__host__ __device__ __forceinline__ size_t splitk_stride(int M, int N) { return ((size_t)M * N + 3) & ~(size_t)3; }
+// Split-K for a grid of `tiles` blocks over `nsteps` K steps: when the tiles leave CUs idle, K is
+// split so that the grid holds about `per_cu` blocks per CU, each split keeping at least
+// `min_steps` steps; the partials must fit the scratch (a.work, or the workspace). BYHIP_Q4_SPLIT
+// forces the number of splits, as does `forced` > 0. Sets a.part / a.split_steps and returns the
+// number of splits (1: none).
+int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps, int forced, int per_cu = 2);
+// y = the sum of the split-K partials in slice order.
+void launch_splitk_sum(const GemmArgs& a, int splits);
+
+// Queues the GEMM on the library stream; K % 32 == 0 is required (callers check). fp16 MFMA: the
+// weights are rounded once to fp16 (exact for F16 weights and for FP4-KM tables whose products
+// are halves; Q4 rounds (q - z) * s).
 void launch_gemm(BFormat fmt, const GemmArgs& a);
+
+// The exact route: each weight formed in fp32 exactly as the reference forms it (Q4
+// ((float)q - z) * s with any scales, zeros and group size; FP4-KM lut[nibble] * lut[16 + byte];
+// F16 halves), fp32 activations as they are (fp16 widened), fp32 products and accumulation in
+// v_mfma_f32_16x16x4_f32. Any K (Q4; FP4-KM and F16 need K % 32 == 0), M, N.
+void launch_gemm_exact(BFormat fmt, const GemmArgs& a);
 
 // The Q4 GEMM kernels by explicit choice (a tuned plan's candidates): kQ4Pipe, the LDS-staged
 // pipelined kernel with `tile` 1..4 (64x128, 64x64, 32x128, 32x64) and `splits`; kQ4Skinny (M <= 32,

@@ -14,8 +14,11 @@
 //   Q4Fast  nibble pairs (k, k+4) of each 8-value word, from one AND-OR against 0x6400
 //   Fp4Km   byte j -> (element j, element j+16), the FP4-KM packing (session_vm.nim:384-388)
 //   others  natural order.
-// fp32 activations are split into hi = fp16(x) and lo = fp16(x - hi) and multiplied twice, which
-// keeps ~22 bits of x; fp16 activations are used as they are.
+// fp32 activations: each row is first brought onto fp16's range by an exact power of two (undone
+// on the output), then split into hi = fp16(x) and lo = fp16(x - hi), ~22 bits of x; with Q4
+// weights the weight's fp16 remainder is staged as well and the products hi*w_hi + lo*w_hi +
+// hi*w_lo keep the fp32 weight, so fp32 activations meet the reference's fp32 tolerance. fp16
+// activations are used as they are, against the weight rounded once to fp16.
 #include <algorithm>
 
 #include "byhip_gemm.h"
@@ -58,6 +61,8 @@ __device__ __forceinline__ void stage_a(const GemmArgs& a, int m, int k0, int se
     }
     float u[8], v[8];
     const bool row_ok = m < a.M;
+    // fp32 activations: the row's power-of-two shift onto fp16's range (exact)
+    const int sh = XF32 && row_ok ? a.row_shift[m] : 0;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
         const int k = k0 + (c == 0 ? eu : ev);
@@ -68,6 +73,8 @@ __device__ __forceinline__ void stage_a(const GemmArgs& a, int m, int k0, int se
                 const float4 p0 = p[0], p1 = p[1];
                 dst[0] = p0.x; dst[1] = p0.y; dst[2] = p0.z; dst[3] = p0.w;
                 dst[4] = p1.x; dst[5] = p1.y; dst[6] = p1.z; dst[7] = p1.w;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dst[i] = __builtin_amdgcn_ldexpf(dst[i], sh);
             } else {
                 const h8 h = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + (size_t)m * a.K + k);
 #pragma unroll
@@ -109,10 +116,15 @@ __device__ __forceinline__ void stage_a(const GemmArgs& a, int m, int k0, int se
 }
 
 // Stages one 32-value weight group of column n (K positions k0g .. k0g+31) into LDS (32 halves).
-template <BFormat F>
+// WLO (Q4 formats with fp32 activations): also the remainder w - fp16(w) as halves into dst_lo, so
+// that hi + lo holds the fp32 weight to ~22 bits (for Q4Fast exactly: (q - z) * s has at most 15
+// significant bits, and the remainder at most 4 at or above 2^-24, the weights being fp16-safe).
+template <BFormat F, bool WLO>
 __device__ __forceinline__ void stage_b(const GemmArgs& a, int n, int k0g, const float* lut_s,
-                                        _Float16* dst) {
-    uint32_t outw[16];
+                                        _Float16* dst, _Float16* dst_lo) {
+    uint32_t outw[16], outl[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) outl[i] = 0u;
     if (n >= a.N || k0g >= a.K) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) outw[i] = 0u;
@@ -129,7 +141,15 @@ __device__ __forceinline__ void stage_b(const GemmArgs& a, int n, int k0g, const
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const h2 q = bits_h2(((dw[w] >> (4 * i)) & 0x000F000Fu) | 0x64006400u);
-                outw[4 * w + i] = h2_bits((q - zz) * ss);
+                const h2 qz = q - zz, hi = qz * ss;
+                outw[4 * w + i] = h2_bits(hi);
+                if constexpr (WLO) {
+                    // (q - z) * s exactly in fp32, less its fp16 rounding: exact in fp16
+                    const float sf = (float)s;
+                    const _Float16 l0 = (_Float16)((float)qz[0] * sf - (float)hi[0]);
+                    const _Float16 l1 = (_Float16)((float)qz[1] * sf - (float)hi[1]);
+                    outl[4 * w + i] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
+                }
             }
     } else if constexpr (F == BFormat::Q4Generic) {
         const uint4 d = *reinterpret_cast<const uint4*>(a.wq + (size_t)n * a.row_bytes + (k0g >> 1));
@@ -142,7 +162,7 @@ __device__ __forceinline__ void stage_b(const GemmArgs& a, int n, int k0g, const
                                : static_cast<const float*>(a.scales)[rowg + gg];
         };
         float s = scale_at(g), z = a.zeros ? a.zeros[rowg + g] : a.zero_value;
-        _Float16 t[32];
+        _Float16 t[32], tl[32];
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
             if (k0g + e >= next) {
@@ -152,11 +172,15 @@ __device__ __forceinline__ void stage_b(const GemmArgs& a, int n, int k0g, const
                 z = a.zeros ? a.zeros[rowg + g] : a.zero_value;
             }
             const uint32_t q = (dw[e >> 3] >> (4 * (e & 7))) & 15u;
-            t[e] = (_Float16)(((float)q - z) * s);
+            const float wf = ((float)q - z) * s;  // the reference's weight
+            t[e] = (_Float16)wf;
+            tl[e] = WLO ? (_Float16)(wf - (float)t[e]) : (_Float16)0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < 16; ++i) {
             outw[i] = (uint32_t)h_bits(t[2 * i]) | ((uint32_t)h_bits(t[2 * i + 1]) << 16);
+            outl[i] = (uint32_t)h_bits(tl[2 * i]) | ((uint32_t)h_bits(tl[2 * i + 1]) << 16);
+        }
     } else if constexpr (F == BFormat::Fp4Km) {
         const size_t kb = (size_t)a.K >> 1;
         const uint4 d = *reinterpret_cast<const uint4*>(a.blob + (size_t)n * kb + (k0g >> 1));
@@ -181,14 +205,23 @@ __device__ __forceinline__ void stage_b(const GemmArgs& a, int n, int k0g, const
     uint4* o = reinterpret_cast<uint4*>(dst);
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = make_uint4(outw[4 * i], outw[4 * i + 1], outw[4 * i + 2], outw[4 * i + 3]);
+    if constexpr (WLO) {
+        uint4* ol = reinterpret_cast<uint4*>(dst_lo);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ol[i] = make_uint4(outl[4 * i], outl[4 * i + 1], outl[4 * i + 2], outl[4 * i + 3]);
+    }
 }
 
 template <BFormat F, bool XF32, int YT>
 __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
     constexpr int PERM = FormatTraits<F>::kPerm;
+    // fp32 activations with Q4 weights: the weights' fp16 remainders too (F16 weights and FP4-KM
+    // tables of halves are exact in one fp16 term)
+    constexpr bool WLO = XF32 && (F == BFormat::Q4Fast || F == BFormat::Q4Generic);
     __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDA];
     __shared__ __attribute__((aligned(16))) _Float16 Al[XF32 ? BM * LDA : 8];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDA];
+    __shared__ __attribute__((aligned(16))) _Float16 Bl[WLO ? BN * LDA : 8];
     __shared__ float lut_s[F == BFormat::Fp4Km ? 272 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -211,11 +244,12 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
     for (int k0 = 0; k0 < a.K; k0 += BK) {
         stage_a<PERM, XF32>(a, m0 + arow, k0, aseg, &As[arow * LDA + 16 * aseg],
                             XF32 ? &Al[arow * LDA + 16 * aseg] : nullptr);
-        stage_b<F>(a, n0 + bcol, k0 + 32 * bhalf, lut_s, &Bs[bcol * LDA + 32 * bhalf]);
+        stage_b<F, WLO>(a, n0 + bcol, k0 + 32 * bhalf, lut_s, &Bs[bcol * LDA + 32 * bhalf],
+                        WLO ? &Bl[bcol * LDA + 32 * bhalf] : nullptr);
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
-            h8 av[2], al[2], bv[4];
+            h8 av[2], al[2], bv[4], bl[4];
             const int kc = kk + 8 * (lane >> 4);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -227,6 +261,7 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
             for (int j = 0; j < 4; ++j) {
                 const int c = wn * 64 + j * 16 + (lane & 15);
                 bv[j] = *reinterpret_cast<const h8*>(&Bs[c * LDA + kc]);
+                if constexpr (WLO) bl[j] = *reinterpret_cast<const h8*>(&Bl[c * LDA + kc]);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -235,6 +270,8 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
                     if constexpr (XF32)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bv[j], acc[i][j], 0, 0, 0);
+                    if constexpr (WLO)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bl[j], acc[i][j], 0, 0, 0);
                 }
         }
         __syncthreads();
@@ -248,9 +285,29 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
-                if (m < a.M && n < a.N) store_y<YT>(a.y, (size_t)m * a.N + n, acc[i][j][r]);
+                if (m < a.M && n < a.N) {
+                    // fp32 activations: undo the row's shift (exact unless the result over- or
+                    // underflows, as the reference's own sum would)
+                    const float v = XF32 ? __builtin_amdgcn_ldexpf(acc[i][j][r], -a.row_shift[m]) : acc[i][j][r];
+                    store_y<YT>(a.y, (size_t)m * a.N + n, v);
+                }
             }
         }
+}
+
+// Per-row shift t of fp32 activations: the row's largest magnitude brought into [2^14, 2^15) (one
+// block per row), so the fp16 hi + lo split of x * 2^t neither overflows nor loses the row's large
+// values to fp16 subnormals.
+__global__ __launch_bounds__(256) void row_range_shift(const float* __restrict__ x, int K, int* __restrict__ out) {
+    __shared__ float part[4];
+    const float* r = x + (size_t)blockIdx.x * K;
+    float mx = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(r[k]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = fp16_range_shift(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])));
 }
 
 // Pipelined Q4 GEMM for the benchmark format: fp16 activations, fp16 scales, one integral zero,
@@ -293,9 +350,6 @@ __device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) { return __b
 __device__ __forceinline__ uint4 perm8(uint4 v) {
     return make_uint4(pair_lo(v.x, v.z), pair_hi(v.x, v.z), pair_lo(v.y, v.w), pair_hi(v.y, v.w));
 }
-
-// Floats between consecutive split-K partials (16-byte aligned).
-__host__ __device__ __forceinline__ size_t splitk_stride(int M, int N) { return ((size_t)M * N + 3) & ~(size_t)3; }
 
 template <int BM, int BN, int YT>
 __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
@@ -947,20 +1001,20 @@ void launch_q4_pipe_shape(const GemmArgs& a, int splits) {
     BYHIP_LAUNCHED("q4_gemm_pipe");
 }
 
-// Split-K for a grid of `tiles` blocks over `nsteps` K steps: when the tiles leave CUs idle, K is
-// split so that the grid holds about `per_cu` blocks per CU, each split keeping at least
-// `min_steps` steps; the partials must fit the workspace. BYHIP_Q4_SPLIT forces the number of
-// splits. Sets a.part / a.split_steps and returns the number of splits (1: none).
-int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps, int forced, int per_cu = 2) {
+}  // namespace
+
+int choose_split(GemmArgs& a, long tiles, int nsteps, int min_steps, int forced, int per_cu) {
     const long cus = compute_units();
     long splits = forced > 0 ? forced : env_int("BYHIP_Q4_SPLIT", 0);
     if (splits < 1)
         splits = tiles >= cus ? 1 : std::min<long>((per_cu * cus + tiles - 1) / tiles, nsteps / min_steps);
-    const long fit = (long)(kWorkspaceBytes / (splitk_stride(a.M, a.N) * sizeof(float)));
+    void* work = a.work ? a.work : workspace();
+    const size_t work_bytes = a.work ? a.work_bytes : kWorkspaceBytes;
+    const long fit = (long)(work_bytes / (splitk_stride(a.M, a.N) * sizeof(float)));
     splits = std::max<long>(1, std::min<long>({splits, (long)nsteps, fit}));
     if (splits == 1) return 1;
     a.split_steps = (int)((nsteps + splits - 1) / splits);
-    a.part = static_cast<float*>(workspace());
+    a.part = static_cast<float*>(work);
     return (nsteps + a.split_steps - 1) / a.split_steps;  // no empty split
 }
 
@@ -974,6 +1028,8 @@ void launch_splitk_sum(const GemmArgs& a, int splits) {
     }
     BYHIP_LAUNCHED("splitk_sum");
 }
+
+namespace {
 
 // Tile choice: 64 x 128, or 32 x 128 when M <= 32, split along K when the tiles leave CUs idle.
 // BYHIP_Q4_TILE=1..4 forces 64x128, 64x64, 32x128, 32x64; a tuned plan passes tile / splits (0:
@@ -1109,9 +1165,22 @@ void launch_fx(const GemmArgs& a) {
 }
 
 template <BFormat F>
-void launch_f(const GemmArgs& a) {
-    if (a.x_dtype == BYHIP_F32) launch_fx<F, true>(a);
-    else launch_fx<F, false>(a);
+void launch_f(const GemmArgs& a0) {
+    if (a0.x_dtype != BYHIP_F32) {
+        launch_fx<F, false>(a0);
+        return;
+    }
+    // fp32 activations: the per-row shifts first, into the scratch
+    GemmArgs a = a0;
+    void* work = a.work ? a.work : workspace();
+    const size_t work_bytes = a.work ? a.work_bytes : kWorkspaceBytes;
+    if ((size_t)a.M * sizeof(int) > work_bytes) fail("byhip: M=%d rows of fp32 activations exceed the scratch", a.M);
+    int* shifts = static_cast<int*>(work);
+    hipLaunchKernelGGL(row_range_shift, dim3((unsigned)a.M), dim3(256), 0, stream(), static_cast<const float*>(a.x), a.K,
+                       shifts);
+    BYHIP_LAUNCHED("row_range_shift");
+    a.row_shift = shifts;
+    launch_fx<F, true>(a);
 }
 
 }  // namespace

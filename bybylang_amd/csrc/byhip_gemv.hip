@@ -22,6 +22,12 @@
 // the fp16 output's own. With fp32 activations the bias is subtracted from the halves first (exact)
 // and x is split into two fp16 terms (hi + lo, ~22 bits). The zero point enters once per chunk as
 // s * (sum x*q - z * sum x).
+//
+// fp32 range: each 32-value chunk of fp32 activations is multiplied by an exact power of two 2^t
+// that brings its largest magnitude into [2^14, 2^15) before the split, and the chunk's partial is
+// multiplied by 2^-t (folded into its scale). So any finite fp32 input keeps its ~22 bits: nothing
+// overflows fp16, and only values more than 2^28 below the chunk's largest reach fp16 subnormals
+// (an absolute error below 2^-39 of that largest value). Non-finite inputs give non-finite outputs.
 #include <algorithm>
 
 #include "byhip_gemv.h"
@@ -72,6 +78,10 @@ __device__ __forceinline__ void load_bytes(rsrc_t r, uint32_t off, uint32_t* w) 
 template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK, int YT>
 __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     constexpr int XS = XF32 ? 2 : 1;
+    // A single fp32 row of more than 4 chunks per lane does not fit the register tile: its
+    // activations are then read from LDS where each weight row uses them.
+    constexpr bool XLDS = M * CPL * XS > 8;
+    static_assert(!XLDS || M == 1, "the launcher slices rows so that only one-row launches read x from LDS");
     constexpr int R = gemv_rows(M, CPL);
     constexpr uint32_t XB = XF32 ? 4 : 2;  // bytes per activation
     constexpr int XW = XF32 ? 8 : 4;       // 16-byte activation loads per 32-value chunk
@@ -181,6 +191,14 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
                     v[4 * t + 2] = __builtin_bit_cast(float, xraw[i][t].z);
                     v[4 * t + 3] = __builtin_bit_cast(float, xraw[i][t].w);
                 }
+                // the chunk onto fp16's range: x * 2^sh; the partial is scaled back by 2^-sh
+                float mx = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 32; ++t) mx = fmaxf(mx, fabsf(v[t]));
+                const int sh = fp16_range_shift(mx);
+#pragma unroll
+                for (int t = 0; t < 32; ++t) v[t] = __builtin_amdgcn_ldexpf(v[t], sh);
+                bias = __builtin_amdgcn_ldexpf(1.0f, -sh);  // the back-scale rides in the bias slot
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -237,28 +255,35 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     __syncthreads();
     if (!rows_live) return;
 
-    uint32_t xp[M][CPL][16];
-    uint32_t xq[XS == 2 ? M : 1][XS == 2 ? CPL : 1][16];
+    // The staged activation pairs of (row m, lane chunk c): held in registers for the whole row
+    // loop when they fit (XLDS false), else read from LDS where each row uses them.
+    constexpr int XM = XLDS ? 1 : M, XCP = XLDS ? 1 : CPL;
+    uint32_t xp[XM][XCP][16];
+    uint32_t xq[XS == 2 ? XM : 1][XS == 2 ? XCP : 1][16];
     float bias[M][CPL], sx[M][CPL];
+    auto read_x = [&](int m, int c, uint32_t* hp, uint32_t* lp) {
+        const int idx = m * G + (int)(coff[c] >> 4);
+        const uint4* sh = reinterpret_cast<const uint4*>(xh + idx * 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint4 u = sh[t];
+            hp[4 * t] = u.x; hp[4 * t + 1] = u.y; hp[4 * t + 2] = u.z; hp[4 * t + 3] = u.w;
+        }
+        if constexpr (XS == 2) {
+            const uint4* sl = reinterpret_cast<const uint4*>(xl + idx * 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint4 u = sl[t];
+                lp[4 * t] = u.x; lp[4 * t + 1] = u.y; lp[4 * t + 2] = u.z; lp[4 * t + 3] = u.w;
+            }
+        }
+    };
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const int idx = m * G + (int)(coff[c] >> 4);
-            const uint4* sh = reinterpret_cast<const uint4*>(xh + idx * 16);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint4 u = sh[t];
-                xp[m][c][4 * t] = u.x; xp[m][c][4 * t + 1] = u.y; xp[m][c][4 * t + 2] = u.z; xp[m][c][4 * t + 3] = u.w;
-            }
-            if constexpr (XS == 2) {
-                const uint4* sl = reinterpret_cast<const uint4*>(xl + idx * 16);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint4 u = sl[t];
-                    xq[m][c][4 * t] = u.x; xq[m][c][4 * t + 1] = u.y; xq[m][c][4 * t + 2] = u.z; xq[m][c][4 * t + 3] = u.w;
-                }
-            }
+            if constexpr (!XLDS) read_x(m, c, xp[m][c], xq[XS == 2 ? m : 0][XS == 2 ? c : 0]);
             bias[m][c] = sums[2 * idx];
             sx[m][c] = sums[2 * idx + 1];
         }
@@ -299,13 +324,18 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
             const float z = ZU ? a.zero_value : __builtin_bit_cast(float, zraw[r][c]);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
+                const uint32_t* hp = xp[XLDS ? 0 : m][XLDS ? 0 : c];
+                const uint32_t* lp = xq[XS == 2 && !XLDS ? m : 0][XS == 2 && !XLDS ? c : 0];
+                if constexpr (XLDS) read_x(m, c, xp[0][0], xq[0][0]);
                 float p = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    p = __builtin_amdgcn_fdot2(bits_h2(xp[m][c][e]), q[e], p, false);
-                    if constexpr (XS == 2) p = __builtin_amdgcn_fdot2(bits_h2(xq[m][c][e]), q[e], p, false);
+                    p = __builtin_amdgcn_fdot2(bits_h2(hp[e]), q[e], p, false);
+                    if constexpr (XS == 2) p = __builtin_amdgcn_fdot2(bits_h2(lp[e]), q[e], p, false);
                 }
-                acc[m] = fmaf(s, (p - bias[m][c]) - z * sx[m][c], acc[m]);
+                // fp32 x: the bias slot holds the chunk's back-scale 2^-sh
+                if constexpr (XS == 2) acc[m] = fmaf(s * bias[m][c], p - z * sx[m][c], acc[m]);
+                else acc[m] = fmaf(s, (p - bias[m][c]) - z * sx[m][c], acc[m]);
             }
         }
 #pragma unroll
@@ -338,7 +368,7 @@ void launch_y(const GemvArgs& a, int y_dtype) {
 
 template <int M, int CPL, bool XF32>
 void launch_szb(const GemvArgs& a, const byhip_q4w* w, bool blk, int y_dtype) {
-    if constexpr (M * CPL * (XF32 ? 2 : 1) > 8) {
+    if constexpr (M > 1 && M * CPL * (XF32 ? 2 : 1) > 8) {
         fail("byhip: internal: GEMV register tile out of range");
     } else {
         const bool sf = blk ? w->blk_scale_f16 : w->scale_f16;
@@ -420,8 +450,9 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     const int K = a.K, G = K >> 5;
     uint32_t* xh = lds;                                      // [G][16] fp16 pairs, high terms
     uint32_t* xl = xh + G * 16;                              // [G][16] low terms
-    float* sums = reinterpret_cast<float*>(xl + G * 16);     // [G] sum of x over the chunk
-    float* ssq_part = sums + G;                              // [256]
+    float* sums = reinterpret_cast<float*>(xl + G * 16);     // [G] sum of the scaled x over the chunk
+    float* facs = sums + G;                                  // [G] the chunk's back-scale 2^-sh
+    float* ssq_part = facs + G;                              // [256]
 
     const int wb = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (tid >> 6));
     const bool live = wb < a.batches;  // uniform in the wave; every wave takes part in the barrier
@@ -525,6 +556,13 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
                 }
             }
         }
+        // the chunk onto fp16's range (x * 2^sh), as in q4_gemv
+        float mx = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) mx = fmaxf(mx, fabsf(v[t]));
+        const int sh = fp16_range_shift(mx);
+#pragma unroll
+        for (int t = 0; t < 32; ++t) v[t] = __builtin_amdgcn_ldexpf(v[t], sh);
         uint32_t p[16], lo[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -547,6 +585,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
             dl[t] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
         }
         sums[idx] = s;
+        facs[idx] = __builtin_amdgcn_ldexpf(1.0f, -sh);
     };
     stage_chunk(tid, xraw, graw);
     if (G > 256) {  // K > 8192: a second chunk per thread (G <= 512)
@@ -591,7 +630,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
                 xp[4 * t] = u.x; xp[4 * t + 1] = u.y; xp[4 * t + 2] = u.z; xp[4 * t + 3] = u.w;
                 xq[4 * t] = w.x; xq[4 * t + 1] = w.y; xq[4 * t + 2] = w.z; xq[4 * t + 3] = w.w;
             }
-            const float sxc = sums[idx];
+            const float sxc = sums[idx], fac = facs[idx];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const uint32_t dw[4] = {wv[j][r][c].x, wv[j][r][c].y, wv[j][r][c].z, wv[j][r][c].w};
@@ -615,7 +654,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
                 float sc = SF16 ? (float)bits_h((uint16_t)sraw[j][r][c]) : __builtin_bit_cast(float, sraw[j][r][c]);
                 sc = cv[c] ? sc : 0.0f;
                 const float z = ZU ? fm.zero_value : __builtin_bit_cast(float, zraw[j][r][c]);
-                acc[r] = fmaf(sc, p - z * sxc, acc[r]);
+                acc[r] = fmaf(sc * fac, p - z * sxc, acc[r]);
             }
         }
 #pragma unroll
@@ -640,7 +679,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
 template <int CPL, int MODE>
 void launch_fused_sz(const FusedArgs& a, bool sf16, bool zu) {
     const int G = a.K / 32;
-    const size_t lds = (size_t)G * 16 * 4 * 2 + (size_t)G * 4 + 256 * 4;
+    const size_t lds = (size_t)G * 16 * 4 * 2 + (size_t)G * 4 * 2 + 256 * 4;
     const dim3 grid((a.batches + 3) / 4);
 #define BYHIP_FUSED_CASE(SF, ZU_) \
     if (sf16 == SF && zu == ZU_) { hipLaunchKernelGGL((q4_gemv_fused<CPL, SF, ZU_, MODE>), grid, dim3(256), lds, stream(), a); }
@@ -654,25 +693,37 @@ void launch_fused_sz(const FusedArgs& a, bool sf16, bool zu) {
 
 }  // namespace
 
+// Activation rows one GEMV launch takes (at most 4): the rows' staged activations fit the register
+// tile (rows x chunks per lane x fp16 terms <= 8, except a single row, which then reads them from
+// LDS), the block's staging (at most 512 chunks) and 64 KB of LDS. 0: not even one row fits.
+int gemv_rows_per_launch(int K, int M, int x_dtype) {
+    const int xs = x_dtype == BYHIP_F32 ? 2 : 1, G = K / 32, cpl = gemv_cpl(K);
+    for (int m = std::min(M, 4); m >= 1; --m) {
+        const size_t lds = (size_t)m * G * (64 * xs + 8);
+        if ((m == 1 || m * xs * cpl <= 8) && m * G <= 512 && lds <= 65536) return m;
+    }
+    return 0;
+}
+
 bool q4_gemv_eligible(const byhip_q4w* w, int M, int x_dtype) {
     if (w->K % 32 != 0 || (w->group != 0 && w->group % 32 != 0)) return false;
-    const int xs = x_dtype == BYHIP_F32 ? 2 : 1;
     const int cpl = gemv_cpl(w->K);
-    const int m = std::min(M, 4);
     // 32-bit buffer offsets (below the out-of-range marker) for weights, scales and activations
     const uint64_t lim = kOutOfRange - 64;
     const bool fits = (uint64_t)w->N * w->row_bytes < lim && (uint64_t)(w->N + 8) * (w->K / 32 + w->gpr) * 4 < lim &&
-                      (uint64_t)m * w->K * 4 < lim;
+                      (uint64_t)4 * w->K * 4 < lim;
     const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0;
-    return fits && aligned && cpl <= 8 && m * xs * cpl <= 8;
+    return fits && aligned && cpl <= 8 && gemv_rows_per_launch(w->K, M, x_dtype) > 0;
 }
 
 void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
     const int cpl = gemv_cpl(w->K);
     const size_t xb = dtype_bytes(x_dtype), yb = dtype_bytes(y_dtype);
     const bool blk = w->sblk != nullptr;
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        const int mm = std::min(4, M - m0);
+    const int step = gemv_rows_per_launch(w->K, M, x_dtype);
+    if (step < 1) fail("byhip: internal: GEMV launched on a shape it does not take (K=%d)", w->K);
+    for (int m0 = 0; m0 < M; m0 += step) {
+        const int mm = std::min(step, M - m0);
         GemvArgs a;
         a.x = static_cast<const uint8_t*>(x) + (size_t)m0 * w->K * xb;
         a.wq = w->wq;
@@ -722,7 +773,7 @@ int q4_fused_check(int mode, const byhip_q4w* const* ws, int n_ws) {
     if (mode == 1 && ws[1]->N != w0->N) return BYHIP_UNSUPPORTED;
     // chunks per lane: 8 at most (4 with gate and up); the staged input fits 64 KB of LDS
     const int G = w0->K / 32;
-    if (gemv_cpl(w0->K) > (mode == 1 ? 4 : 8) || (size_t)G * 132 + 1024 > 65536) return BYHIP_UNSUPPORTED;
+    if (gemv_cpl(w0->K) > (mode == 1 ? 4 : 8) || (size_t)G * 136 + 1024 > 65536) return BYHIP_UNSUPPORTED;
     return BYHIP_OK;
 }
 

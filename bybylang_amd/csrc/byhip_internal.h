@@ -61,6 +61,9 @@ void device_free(void* p);
 void check_span(const void* p, size_t need, const char* what);
 // Reads `bytes` at `p` to the host, from the mirror when there is one, else with a stream wait.
 void read_small(const void* p, size_t off, void* dst, size_t bytes);
+// The same, but returns false instead of waiting when there is no host copy and a session is being
+// recorded (a recording cannot wait for the device).
+bool try_read_small(const void* p, size_t off, void* dst, size_t bytes);
 
 template <class F>
 int guard(F&& f) {
@@ -113,4 +116,8 @@ struct byhip_q4w {
     void* sblk = nullptr;
     float* zblk = nullptr;
     int blk_scale_f16 = 0;
+    // Every (q - z) * s lies in fp16's normal range (or is 0), so the fp16 MFMA kernels may take
+    // these weights (rounding each product once); else the exact fp32 route runs them. Weights
+    // built from micro-VM slots are not classified (0).
+    int f16_safe = 0;
 };

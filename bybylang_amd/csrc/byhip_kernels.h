@@ -67,6 +67,13 @@ __device__ __forceinline__ float wave_sum_lane0(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Power-of-two exponent t that brings a magnitude `mx` (>= 0) into [2^14, 2^15) as mx * 2^t when mx
+// is a normal fp32 value (subnormals land below, inf and NaN stay what they are): the shift that
+// maps a chunk of fp32 activations onto fp16's range before it is split into fp16 hi + lo terms.
+__device__ __forceinline__ int fp16_range_shift(float mx) {
+    return 141 - (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFFu);
+}
+
 // Buffer resource over `bytes` bytes at `p`: raw buffer loads take 32-bit offsets and return 0 for
 // any offset past the end (hardware range check), so edge tiles need no clamps.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;

@@ -15,7 +15,8 @@ enum Q4PlanKind : int {
     kPlanGemm = 5,     // the general LDS-staged MFMA GEMM
     kPlanBig = 6,      // the 128 x 256 prefill tile
     kPlanWide = 7,     // the 64 x 128 skinny prefill tile
-    kPlanLast = kPlanWide
+    kPlanExact = 8,    // the exact fp32 MFMA GEMM
+    kPlanLast = kPlanExact
 };
 struct Q4Plan {
     int kind = 0;

@@ -4,9 +4,10 @@
 // (group 0: g = 0), q the nibble k of row n with even k in the low nibble: the reference's
 // cpu_kernels_impl.inc:293-319, gpubackend.nim:288-311 and cpu_vm.c:420-482, accumulated in fp32.
 //
-// Decode GEMV (M <= 8): byhip_gemv.hip. Larger M: the fp16 MFMA GEMM of byhip_gemm.hip. Shapes
-// neither takes (K or the group not a multiple of 32, unaligned buffers): q4_generic below, which
-// forms the reference's per-element weight ((float)q - z) * s in fp32.
+// Decode GEMV (M <= 8): byhip_gemv.hip. Larger M: the fp16 MFMA GEMM of byhip_gemm.hip for weights
+// whose products stay in fp16's range, else the exact fp32 GEMM of byhip_exact.hip. Decode shapes
+// the GEMV does not take (K or the group not a multiple of 32, unaligned buffers): q4_generic below,
+// which forms the reference's per-element weight ((float)q - z) * s in fp32.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -77,23 +78,55 @@ __global__ void q4_unpack(const uint8_t* __restrict__ wq, size_t row_bytes, int 
     }
 }
 
-// Classification of the scales and zeros of a resident upload, per block: flags[2b] = every
-// scale in the block is finite and converts to fp16 exactly, flags[2b + 1] = every zero equals
-// zeros[0] bit for bit. The host ANDs the block flags.
+// Classification of the scales and zeros of a resident upload, per block b, in flags[8b .. 8b+7]:
+//   0  every scale is finite and converts to fp16 exactly
+//   1  every zero equals zeros[0] bit for bit
+//   2  every scale and zero is finite
+//   3  the largest |scale| (float bits)
+//   4  the smallest nonzero |scale| (float bits; +inf when every scale is zero)
+//   5, 6  the smallest and largest zero (float bits)
+// The host combines the blocks.
 __global__ __launch_bounds__(256) void q4_classify(const float* __restrict__ sc, const float* __restrict__ ze,
                                                    size_t ng, int* __restrict__ flags) {
+    __shared__ float red[4][4];
     const uint32_t z0 = __builtin_bit_cast(uint32_t, ze[0]);
-    int ok_s = 1, ok_z = 1;
+    int ok_s = 1, ok_z = 1, fin = 1;
+    float smax = 0.0f, smin = __builtin_inff(), zmin = __builtin_inff(), zmax = -__builtin_inff();
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < ng; i += (size_t)gridDim.x * 256) {
-        const float s = sc[i];
+        const float s = sc[i], z = ze[i];
         ok_s &= (__builtin_isfinite(s) && (float)(_Float16)s == s) ? 1 : 0;
-        ok_z &= __builtin_bit_cast(uint32_t, ze[i]) == z0 ? 1 : 0;
+        ok_z &= __builtin_bit_cast(uint32_t, z) == z0 ? 1 : 0;
+        fin &= (__builtin_isfinite(s) && __builtin_isfinite(z)) ? 1 : 0;
+        const float as = fabsf(s);
+        smax = fmaxf(smax, as);
+        if (as > 0.0f) smin = fminf(smin, as);
+        zmin = fminf(zmin, z);
+        zmax = fmaxf(zmax, z);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        smax = fmaxf(smax, __shfl_xor(smax, o, kWave));
+        smin = fminf(smin, __shfl_xor(smin, o, kWave));
+        zmin = fminf(zmin, __shfl_xor(zmin, o, kWave));
+        zmax = fmaxf(zmax, __shfl_xor(zmax, o, kWave));
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[0][w] = smax; red[1][w] = smin; red[2][w] = zmin; red[3][w] = zmax;
     }
     ok_s = __syncthreads_and(ok_s);
     ok_z = __syncthreads_and(ok_z);
+    fin = __syncthreads_and(fin);
     if (threadIdx.x == 0) {
-        flags[2 * blockIdx.x] = ok_s;
-        flags[2 * blockIdx.x + 1] = ok_z;
+        int* f = flags + 8 * blockIdx.x;
+        f[0] = ok_s;
+        f[1] = ok_z;
+        f[2] = fin;
+        f[3] = __builtin_bit_cast(int, fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])));
+        f[4] = __builtin_bit_cast(int, fminf(fminf(red[1][0], red[1][1]), fminf(red[1][2], red[1][3])));
+        f[5] = __builtin_bit_cast(int, fminf(fminf(red[2][0], red[2][1]), fminf(red[2][2], red[2][3])));
+        f[6] = __builtin_bit_cast(int, fmaxf(fmaxf(red[3][0], red[3][1]), fmaxf(red[3][2], red[3][3])));
+        f[7] = 0;
     }
 }
 
@@ -131,6 +164,12 @@ __global__ __launch_bounds__(256) void q4_pack_scales(const float* __restrict__ 
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+float bits_float(int v) {
+    float f;
+    memcpy(&f, &v, sizeof f);
+    return f;
+}
+
 void validate_q4_shape(int K, int N, int group, int gpr) {
     if (K <= 0 || N <= 0) fail("byhip: Q4 weights need K > 0 and N > 0 (K=%d N=%d)", K, N);
     if (group < 0 || gpr <= 0) fail("byhip: Q4 group_size %d / groups_per_row %d invalid", group, gpr);
@@ -148,8 +187,8 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
     const size_t row_bytes = (size_t)(K + 1) / 2;
     const size_t ng = (size_t)N * gpr;
     const int cblocks = (int)std::min<size_t>((ng + 255) / 256, 1024);
-    int* d_flags = static_cast<int*>(device_alloc((size_t)cblocks * 2 * sizeof(int)));
-    std::vector<int> flags((size_t)cblocks * 2);
+    int* d_flags = static_cast<int*>(device_alloc((size_t)cblocks * 8 * sizeof(int)));
+    std::vector<int> flags((size_t)cblocks * 8);
     float zero0 = 0.0f;
     try {
         hipLaunchKernelGGL(q4_classify, dim3(cblocks), dim3(256), 0, stream(), d_sc, d_ze, ng, d_flags);
@@ -162,11 +201,24 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
         throw;
     }
     device_free(d_flags);
-    bool sf16 = true, zu = true;
+    bool sf16 = true, zu = true, finite = true;
+    float smax = 0.0f, smin = INFINITY, zmin = INFINITY, zmax = -INFINITY;
     for (int b = 0; b < cblocks; ++b) {
-        sf16 = sf16 && flags[2 * b];
-        zu = zu && flags[2 * b + 1];
+        const int* f = &flags[8 * b];
+        sf16 = sf16 && f[0];
+        zu = zu && f[1];
+        finite = finite && f[2];
+        smax = std::fmax(smax, bits_float(f[3]));
+        smin = std::fmin(smin, bits_float(f[4]));
+        zmin = std::fmin(zmin, bits_float(f[5]));
+        zmax = std::fmax(zmax, bits_float(f[6]));
     }
+    // The fp16 MFMA kernels round (q - z) * s to fp16 (one rounding, 2^-11 relative): they take the
+    // weights only when every such product stays in fp16's normal range, so none overflows and
+    // none loses more than that to subnormals. Otherwise the exact fp32 route runs them.
+    const float qz = std::fmax(std::fmax(std::fabs(zmin), std::fabs(zmax)),
+                               std::fmax(std::fabs(15.0f - zmin), std::fabs(15.0f - zmax)));
+    const bool f16_safe = finite && (double)smax * qz <= 65504.0 && (smin == INFINITY || smin >= 0x1p-14f);
     const size_t wq_bytes = (size_t)N * row_bytes;
     const size_t s_bytes = ng * (sf16 ? 2 : 4);
     const size_t z_bytes = zu ? 0 : ng * 4;
@@ -190,6 +242,7 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
     w->sblk = blk ? base + o_sb : nullptr;
     w->zblk = blk && !zu ? reinterpret_cast<float*>(base + o_zb) : nullptr;
     w->blk_scale_f16 = sf16;
+    w->f16_safe = f16_safe;
     try {
         BYHIP_HIP(hipMemcpyAsync(w->wq, wq_src, wq_bytes, wq_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                                  stream()));
@@ -292,7 +345,14 @@ bool q4_fast(const byhip_q4w* w) {
     return w->scale_f16 && zeros_integral(w) && (w->group == 0 || w->group % 32 == 0);
 }
 
-void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
+// Routes y = x . W^T. Decode shapes (M <= 8) take the GEMV, whose arithmetic is exact (fp32 scales,
+// zeros and sums; fp32 activations kept to ~22 bits over their whole range), or the per-element
+// kernel when the GEMV does not take the shape. Larger M takes the fp16 MFMA kernels when the
+// weights are fp16-safe (each (q - z) * s rounded once to fp16, byhip_q4w::f16_safe) and `exact`
+// is not asked for, else the exact fp32 GEMM. BYHIP_Q4_ROUTE forces a route: 1 GEMV, 2 GEMM (fp16
+// when safe, else exact), 3 per-element, 4 exact GEMM.
+void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, bool exact,
+                    void* work, size_t work_bytes) {
     if (!w) fail("byhip: null Q4 weights");
     if (x_dtype != BYHIP_F32 && x_dtype != BYHIP_F16) fail("byhip: Q4 activations must be F32 or F16");
     if (y_dtype != BYHIP_F32 && y_dtype != BYHIP_F16 && y_dtype != BYHIP_BF16)
@@ -300,39 +360,32 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
     if (M <= 0) fail("byhip: Q4 matmul needs M > 0 (M=%d)", M);
     check_span(x, (size_t)M * w->K * dtype_bytes(x_dtype), "Q4 activations");
     check_span(y, (size_t)M * w->N * dtype_bytes(y_dtype), "Q4 output");
-    const int mode = env_int("BYHIP_Q4_ROUTE", 0);  // 0 auto, 1 GEMV, 2 GEMM, 3 generic
-    // A plan chosen by byhip_q4_prepare for this shape, unless a route is forced.
+    const int mode = env_int("BYHIP_Q4_ROUTE", 0);
+    GemmArgs ga = q4_gemm_args(x, x_dtype, w, y, y_dtype, M);
+    ga.work = work;
+    ga.work_bytes = work_bytes;
+    // A plan chosen by byhip_q4_prepare for this shape, unless a route is forced or exactness asked.
     Q4Plan plan;
-    if (mode == 0 && q4_lookup_plan(w, M, x_dtype, &plan) && q4_run_plan(plan, x, x_dtype, w, y, y_dtype, M)) return;
+    if (mode == 0 && !exact && !work && q4_lookup_plan(w, M, x_dtype, &plan) &&
+        q4_run_plan(plan, x, x_dtype, w, y, y_dtype, M))
+        return;
     // The vector kernels read 16-byte words of weights and activations.
     const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
-    if (!aligned) {
-        launch_generic(x, x_dtype, w, y, y_dtype, M);
-        return;
-    }
-    const bool gemm_ok = w->K % 32 == 0;
-    if (mode == 3 || (mode == 0 && !gemm_ok && !q4_gemv_eligible(w, M, x_dtype))) {
-        launch_generic(x, x_dtype, w, y, y_dtype, M);
-        return;
-    }
-    const bool want_gemv = mode == 1 || (mode == 0 && M <= 8);
-    if (want_gemv && q4_gemv_eligible(w, M, x_dtype)) {
-        launch_q4_gemv(x, x_dtype, w, y, y_dtype, M);
-        return;
-    }
-    // Decode shapes the GEMV does not take (groups not a multiple of 32, very long K) stay on the
-    // exact per-element kernel rather than rounding weights to fp16 for the MFMA.
-    if (!gemm_ok || (mode <= 1 && M <= 8)) {
-        launch_generic(x, x_dtype, w, y, y_dtype, M);
-        return;
-    }
-    launch_gemm(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic, q4_gemm_args(x, x_dtype, w, y, y_dtype, M));
+    const bool gemv = aligned && q4_gemv_eligible(w, M, x_dtype);
+    if (mode == 3) return launch_generic(x, x_dtype, w, y, y_dtype, M);
+    if (mode == 4) return launch_gemm_exact(BFormat::Q4Generic, ga);
+    if (gemv && (mode == 1 || (mode == 0 && M <= 8))) return launch_q4_gemv(x, x_dtype, w, y, y_dtype, M);
+    // Decode shapes the GEMV does not take stay on the exact per-element kernel.
+    if (M <= 8 && mode != 2) return launch_generic(x, x_dtype, w, y, y_dtype, M);
+    if (!exact && w->f16_safe && aligned && w->K % 32 == 0)
+        return launch_gemm(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic, ga);
+    launch_gemm_exact(BFormat::Q4Generic, ga);
 }
 
 }  // namespace
 
-void q4_matmul_run(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
-    q4_matmul_impl(x, x_dtype, w, y, y_dtype, M);
+void q4_matmul_run(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, bool exact) {
+    q4_matmul_impl(x, x_dtype, w, y, y_dtype, M, exact, nullptr, 0);
 }
 
 bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
@@ -340,6 +393,9 @@ bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w
     switch (p.kind) {
     case kPlanGeneric:
         launch_generic(x, x_dtype, w, y, y_dtype, M);
+        return true;
+    case kPlanExact:
+        launch_gemm_exact(BFormat::Q4Generic, q4_gemm_args(x, x_dtype, w, y, y_dtype, M));
         return true;
     case kPlanGemv:
         if (!aligned || M > 8 || !q4_gemv_eligible(w, M, x_dtype)) return false;
@@ -350,7 +406,8 @@ bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w
     case kPlanGemm:
     case kPlanBig:
     case kPlanWide: {
-        if (!aligned || w->K % 32 != 0) return false;
+        // fp16 MFMA kernels: only for weights whose products stay in fp16's normal range
+        if (!aligned || w->K % 32 != 0 || !w->f16_safe) return false;
         const int kind = p.kind == kPlanPipe     ? kQ4Pipe
                          : p.kind == kPlanSkinny ? kQ4Skinny
                          : p.kind == kPlanBig    ? kQ4Big
@@ -424,14 +481,14 @@ int byhip_q4_resident_info(const byhip_q4w* w, byhip_q4w_info* out) {
         if (!w || !out) fail("byhip: null argument");
         out->K = w->K; out->N = w->N; out->group_size = w->group; out->groups_per_row = w->gpr;
         out->scale_is_f16 = w->scale_f16; out->zero_uniform = w->zero_uniform;
-        out->zero_value = w->zero_value; out->device_bytes = w->bytes;
+        out->zero_value = w->zero_value; out->device_bytes = w->bytes; out->f16_safe = w->f16_safe;
     });
 }
 
 int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
     return guard([&] {
         enter_compute();
-        q4_matmul_impl(x, x_dtype, w, y, y_dtype, M);
+        q4_matmul_impl(x, x_dtype, w, y, y_dtype, M, false, nullptr, 0);
     });
 }
 
@@ -483,7 +540,7 @@ int byhip_gpu_matmul_q4(const float* a, const uint8_t* wq, const float* scales, 
             dx = device_alloc((size_t)M * K * 4);
             dy = device_alloc((size_t)M * N * 4);
             BYHIP_HIP(hipMemcpyAsync(dx, a, (size_t)M * K * 4, hipMemcpyHostToDevice, stream()));
-            q4_matmul_impl(dx, BYHIP_F32, w, dy, BYHIP_F32, M);
+            q4_matmul_impl(dx, BYHIP_F32, w, dy, BYHIP_F32, M, false, nullptr, 0);
             BYHIP_HIP(hipMemcpyAsync(c, dy, (size_t)M * N * 4, hipMemcpyDeviceToHost, stream()));
             BYHIP_HIP(hipStreamSynchronize(stream()));
         } catch (...) {

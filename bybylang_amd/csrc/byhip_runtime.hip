@@ -36,6 +36,7 @@ struct State {
     bool timing = false;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     double gpu_seconds = 0.0;
+    double realtime_hz = 0.0;  // rate of the counter the timing marks read
     // record / replay (sessionBeginRecording .. sessionFreeRecording, gpubackend.nim:2502-2552)
     bool recording = false;
     std::vector<hipGraphExec_t> recordings;  // id -> executable graph (null once freed)
@@ -48,6 +49,11 @@ State& st() {
 }
 
 thread_local std::string t_last_error;
+
+// Timing marks: one thread stores the GPU's constant-rate realtime counter (s_memrealtime, at
+// hipDeviceAttributeWallClockRate) with an ordinary vector store.
+__device__ unsigned long long g_marks[2];
+__global__ void timing_mark(int which) { g_marks[which] = __builtin_amdgcn_s_memrealtime(); }
 std::atomic<int> g_fault_inject{0};
 
 }  // namespace
@@ -152,6 +158,19 @@ void check_span(const void* p, size_t need, const char* what) {
     // Not one of ours (memory from another allocator): the caller vouches for the size.
 }
 
+bool try_read_small(const void* p, size_t off, void* dst, size_t bytes) {
+    if (const std::vector<uint8_t>* m = host_mirror(p)) {
+        if (off + bytes <= m->size()) {
+            memcpy(dst, m->data() + off, bytes);
+            return true;
+        }
+    }
+    if (st().recording) return false;
+    BYHIP_HIP(hipStreamSynchronize(stream()));
+    BYHIP_HIP(hipMemcpy(dst, static_cast<const uint8_t*>(p) + off, bytes, hipMemcpyDeviceToHost));
+    return true;
+}
+
 void read_small(const void* p, size_t off, void* dst, size_t bytes) {
     if (const std::vector<uint8_t>* m = host_mirror(p)) {
         if (off + bytes <= m->size()) {
@@ -198,6 +217,9 @@ int byhip_init(int device) {
         BYHIP_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
         BYHIP_HIP(hipEventCreate(&s.ev_begin));
         BYHIP_HIP(hipEventCreate(&s.ev_end));
+        int khz = 0;
+        BYHIP_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
+        s.realtime_hz = khz * 1e3;
         BYHIP_HIP(hipMalloc(&s.workspace, kWorkspaceBytes));
         s.device = device;
         s.inited = true;
@@ -512,6 +534,60 @@ int byhip_session_replay(int id, int times) {
             BYHIP_HIP(hipEventElapsedTime(&ms, s.ev_begin, s.ev_end));
             s.gpu_seconds += ms * 1e-3;
         }
+    });
+}
+
+int byhip_session_replay_after(int pre_id, int pre_times, int id, int times) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) fail("byhip: replay runs outside a session");
+        for (int r : {pre_id, id})
+            if (r < 0 || r >= (int)s.recordings.size() || !s.recordings[r]) fail("byhip: no recording %d", r);
+        if (pre_times < 1 || times < 1) fail("byhip: replay counts %d, %d", pre_times, times);
+        // Everything is queued before the first wait: while the lead-in runs, the host has already
+        // queued the begin event and the timed launches behind it.
+        for (int i = 0; i < pre_times; ++i) BYHIP_HIP(hipGraphLaunch(s.recordings[pre_id], s.stream));
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+        for (int i = 0; i < times; ++i) BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        BYHIP_HIP(hipStreamSynchronize(s.stream));
+        if (s.timing) {
+            float ms = 0.0f;
+            BYHIP_HIP(hipEventElapsedTime(&ms, s.ev_begin, s.ev_end));
+            s.gpu_seconds += ms * 1e-3;
+        }
+    });
+}
+
+int byhip_session_mark(int which) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (!s.recording) fail("byhip: a mark is recorded inside a recording");
+        if (which != 0 && which != 1) fail("byhip: mark %d (0: begin, 1: end)", which);
+        hipLaunchKernelGGL(timing_mark, dim3(1), dim3(1), 0, s.stream, which);
+        BYHIP_LAUNCHED("timing_mark");
+    });
+}
+
+int byhip_session_replay_marked(int id) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) fail("byhip: replay runs outside a session");
+        if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id]) fail("byhip: no recording %d", id);
+        const unsigned long long unset[2] = {0, 0};
+        BYHIP_HIP(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_marks), unset, sizeof unset, 0, hipMemcpyHostToDevice, s.stream));
+        BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
+        unsigned long long t[2] = {0, 0};
+        BYHIP_HIP(hipMemcpyFromSymbolAsync(t, HIP_SYMBOL(g_marks), sizeof t, 0, hipMemcpyDeviceToHost, s.stream));
+        BYHIP_HIP(hipStreamSynchronize(s.stream));
+        if (!t[0] || !t[1] || t[1] < t[0]) fail("byhip: recording %d holds no pair of timing marks", id);
+        if (s.timing) s.gpu_seconds += (double)(t[1] - t[0]) / s.realtime_hz;
     });
 }
 

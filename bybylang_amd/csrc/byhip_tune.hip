@@ -85,6 +85,7 @@ std::string plan_name(const Q4Plan& p) {
     case kPlanWide:
         snprintf(buf, sizeof buf, "wide-s%d", p.splits);
         return buf;
+    case kPlanExact: return "exact";
     default: return "none";
     }
 }
@@ -189,6 +190,7 @@ std::vector<Candidate> candidates(int mt, int x_dtype) {
         }
     }
     c.push_back({{kPlanGemm, 0, 0}, 3e-3f});
+    c.push_back({{kPlanExact, 0, 0}, 1e-4f});
     return c;
 }
 

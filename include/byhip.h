@@ -127,6 +127,19 @@ int byhip_session_last_recording(void);
 /* sessionReplay: launches recording `id` `times` times back to back (outside a session), then
  * waits; counted by byhip_session_gpu_seconds() when timing is on. */
 int byhip_session_replay(int id, int times);
+/* A measurement form of sessionReplay with no counterpart in the reference: launches recording
+ * `pre_id` `pre_times` times (untimed), then recording `id` `times` times right behind it, and
+ * counts only the latter in byhip_session_gpu_seconds(). All launches are queued before the one
+ * wait, so the timed events never include the host's launch latency. */
+int byhip_session_replay_after(int pre_id, int pre_times, int id, int times);
+/* Measurement marks, with no counterpart in the reference: inside a recording,
+ * byhip_session_mark(0) and (1) record a one-thread kernel that stores the GPU's constant-rate
+ * realtime counter into the library's begin and end slots; byhip_session_replay_marked(id) launches
+ * the recording once, waits, and counts the time between the two stores in
+ * byhip_session_gpu_seconds() (timing on). The slots are the library's: one marked replay at a
+ * time. */
+int byhip_session_mark(int which);
+int byhip_session_replay_marked(int id);
 /* sessionFreeRecording. */
 int byhip_session_free_recording(int id);
 
@@ -141,6 +154,9 @@ typedef struct byhip_q4w_info {
     int zero_uniform;   /* one zero point for every group (its value in zero_value) */
     float zero_value;
     size_t device_bytes;
+    /* every (q - zero) * scale lies in fp16's normal range (or is 0): the fp16 MFMA kernels may
+     * take these weights at M > 8; otherwise the exact fp32 GEMM does */
+    int f16_safe;
 } byhip_q4w_info;
 
 /* residentUploadQ4 (gpubackend.nim:2883-2919) and residentUploadQ4Mapped (2961-2998): host wq
@@ -162,7 +178,10 @@ int byhip_q4_resident_info(const byhip_q4w* w, byhip_q4w_info* out);
 /* sessionMatmulQ4 (gpubackend.nim:3000-3061): y[M, N] = x[M, K] . W^T on device buffers,
  * computing sum_k x[m,k] * (q[n,k] - zero[n,g]) * scale[n,g] (cpu_kernels_impl.inc:293-319,
  * cpu_vm.c:420-482) with fp32 accumulation. x_dtype: BYHIP_F32 or BYHIP_F16; y_dtype: BYHIP_F32,
- * BYHIP_F16 or BYHIP_BF16. M <= 8 runs the decode GEMV, larger M the MFMA GEMM. */
+ * BYHIP_F16 or BYHIP_BF16. M <= 8 runs the decode GEMV; larger M the fp16 MFMA GEMMs when the
+ * weights are fp16-safe (byhip_q4w_info.f16_safe), else the exact fp32 GEMM. fp32 activations
+ * keep the reference's fp32 tolerance on every route (1e-4 of max(1, |y|max)); fp16 activations
+ * at M > 8 use weights rounded once to fp16. */
 int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
 
 /* residentPrepareQ4 (gpubackend.nim:2871-2880; vulkanPrepareQ4Tuned, q4_autotune.nim:387-543):
@@ -239,8 +258,12 @@ int byhip_tile_gemm_ready(int f16, int tensor_core);
  * OP_Q4_GEMV and OP_Q4_COOP_GEMM, decoded with the rules of nimf_cpu_vm_run_slots
  * (cpu_vm.c:420-628) and tileGemmShape (tile_gemm.nim:68-78). Slots are device pointers; lengths
  * are in the reference's units (mem, lut, input: floats; u8: bytes). `rows` > 0 overrides an
- * M = 0 header (a dispatch's row count); with rows = 0, M = 0 means input_len / K. The program's
- * remaining words may only be tile ops, barriers, NOPs and HALT. */
+ * M = 0 header (a dispatch's row count); with rows = 0, M = 0 means input_len / K. A rejected
+ * program returns BYHIP_ERROR with the reference's own message ("CPU VM unsupported tile GEMM
+ * (format 0 K 48 N 16)", "CPU VM q4_coop_store out of range: 64", ...), checked in its order, and
+ * leaves in `mem` the outputs the reference writes before it stops. The Q4 shape ops run the exact
+ * routes (fp32 arithmetic, as in the reference). The program's remaining words may only be tile
+ * ops, barriers, NOPs and HALT (else BYHIP_UNSUPPORTED). */
 int byhip_program_dispatch(const uint32_t* words, int n_words, void* mem, size_t mem_len,
                            const void* u8, size_t u8_len, const void* lut, size_t lut_len,
                            const void* input, size_t input_len, int rows);
