@@ -81,6 +81,7 @@ SIGNATURES = {
     "byhip_q4_resident_free": (_I, [_VP]),
     "byhip_q4_resident_info": (_I, [_VP, C.POINTER(Q4WInfo)]),
     "byhip_q4_matmul": (_I, [_VP, _I, _VP, _VP, _I, _I]),
+    "byhip_q4_matmul_static": (_I, [_VP, _I, _VP, _VP, _I, _I]),
     "byhip_q4_matmul_fused": (_I, [_I, _FP, _VP, _I, _VP, _I, _FP, _I, _FP, C.c_float, _I]),
     "byhip_q4_prepare": (_I, [_VP, _I, _I]),
     "byhip_q4_plan_info": (_I, [_VP, _I, _I, C.c_char_p, _I, C.POINTER(_I)]),

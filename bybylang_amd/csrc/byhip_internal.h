@@ -46,6 +46,8 @@ int compute_units();
 // stream uses it in stream order.
 constexpr size_t kWorkspaceBytes = 32u << 20;
 void* workspace();
+// Takes the device address of byhip_q4_matmul_static's scratch array on `device` (current).
+void static_scratch_setup(int device);
 // Whether a session (or a recording) is open.
 bool session_open();
 // Properties of the initialised device.

@@ -27,6 +27,10 @@ struct Q4Plan {
 // Queues y = x . W^T with the kernel the plan names; false, queueing nothing, when that kernel
 // does not take this call (the arguments were validated by the caller).
 bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
+// byhip_q4_matmul's routing with the kernels' scratch (split-K partials, per-row activation shifts)
+// in `work` (work_bytes) instead of the library workspace; tuned plans are not consulted.
+void q4_matmul_run_scratch(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, void* work,
+                           size_t work_bytes);
 // The plan byhip_q4_prepare chose for these weights, this M's class and activation dtype, if any.
 bool q4_lookup_plan(const byhip_q4w* w, int M, int x_dtype, Q4Plan* out);
 

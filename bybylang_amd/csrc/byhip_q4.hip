@@ -388,6 +388,11 @@ void q4_matmul_run(const void* x, int x_dtype, const byhip_q4w* w, void* y, int 
     q4_matmul_impl(x, x_dtype, w, y, y_dtype, M, exact, nullptr, 0);
 }
 
+void q4_matmul_run_scratch(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, void* work,
+                           size_t work_bytes) {
+    q4_matmul_impl(x, x_dtype, w, y, y_dtype, M, false, work, work_bytes);
+}
+
 bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
     const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     switch (p.kind) {

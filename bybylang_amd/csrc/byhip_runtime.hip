@@ -221,6 +221,7 @@ int byhip_init(int device) {
         BYHIP_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
         s.realtime_hz = khz * 1e3;
         BYHIP_HIP(hipMalloc(&s.workspace, kWorkspaceBytes));
+        static_scratch_setup(device);
         s.device = device;
         s.inited = true;
     });

@@ -184,6 +184,15 @@ int byhip_q4_resident_info(const byhip_q4w* w, byhip_q4w_info* out);
  * at M > 8 use weights rounded once to fp16. */
 int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
 
+/* No counterpart in the reference: byhip_q4_matmul for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results; tuned plans are not consulted. The kernels' scratch (split-K
+ * partial sums, per-row shifts of fp32 activations) is a 16 MiB device array inside the library,
+ * one per GPU, set up by byhip_init: the call allocates nothing. More than 4,194,304 rows of fp32
+ * activations at M > 8 are rejected (BYHIP_ERROR). Calls on one GPU share the array: calls that
+ * overlap (other threads or streams) race on it. */
+int byhip_q4_matmul_static(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M);
+
 /* residentPrepareQ4 (gpubackend.nim:2871-2880; vulkanPrepareQ4Tuned, q4_autotune.nim:387-543):
  * chooses the kernel byhip_q4_matmul uses for these weights, this M's class (1; 2..32; 33..128;
  * more, tuned at M = 1, 32, 64 and 256) and activation dtype (BYHIP_F32 is the reference's session

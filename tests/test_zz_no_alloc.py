@@ -1,0 +1,66 @@
+"""byhip_q4_matmul_static, the Q4 matmul entry point that allocates nothing, against
+byhip_q4_matmul through the C ABI.
+
+The shapes take the routes that use scratch: split-K on the skinny (M = 32) and large-tile
+(M = 256) GEMMs, the per-row shifts of fp32 activations, the exact GEMM's split-K, and the GEMV.
+Each shape runs twice in a row on the static entry point, the second time with a smaller input, so
+the second call finds the first call's contents in the shared scratch. Bar: bit-identical to
+byhip_q4_matmul when both take the same split (they share the kernels), else the parity tiers.
+"""
+import numpy as np
+import pytest
+
+from bybylang_amd import _abi, synth
+from parity import REF_TOL, TIER_F32_ACC, ref_check, tier_check
+
+pytestmark = pytest.mark.gpu
+
+
+def call(hip, fn, x, x_dtype, w, M, N, y_dtype):
+    y = hip.DeviceBuffer(M * N * (4 if y_dtype == hip.F32 else 2))
+    _abi.check(fn(x.ptr, x_dtype, w.handle, y.ptr, y_dtype, M), "q4 matmul")
+    return y.read(hip.np_dtype(y_dtype), M * N).astype(np.float32).reshape(M, N)
+
+
+@pytest.mark.parametrize("shape", [
+    # (M first call, M second call, K, N, x dtype, y dtype, scales)
+    (32, 16, 4096, 4096, "f16", "f16", "f16"),      # skinny GEMM, split-K
+    (256, 130, 4096, 6144, "f16", "f16", "f16"),    # large tile, split-K
+    (64, 24, 1024, 512, "f32", "f32", "f16"),       # fp32 activations: per-row shifts
+    (48, 12, 1024, 384, "f32", "f32", "tiny"),      # exact GEMM (weights outside fp16), split-K
+    (4, 1, 4096, 2048, "f16", "f32", "f16"),        # GEMV (no scratch)
+])
+def test_static_entry_matches_q4_matmul(hip, shape):
+    M1, M2, K, N, xd, yd, scales = shape
+    g = synth.rng(9900 + M1)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    if scales == "tiny":
+        sc = (sc * np.float32(1e-9)).astype(np.float32)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    lib = _abi.load()
+    xt = hip.F16 if xd == "f16" else hip.F32
+    yt = hip.F16 if yd == "f16" else hip.F32
+    for M in (M1, M2):
+        x = synth.activations(g, M, K, np.float16 if xd == "f16" else np.float32)
+        xb = hip.DeviceBuffer.from_array(x.reshape(-1))
+        print(f"static entry M={M} K={K} N={N} x={xd} y={yd} scales={scales}", flush=True)
+        want = call(hip, lib.byhip_q4_matmul, xb, xt, w, M, N, yt)
+        got = call(hip, lib.byhip_q4_matmul_static, xb, xt, w, M, N, yt)
+        if not np.array_equal(got, want):
+            if yd == "f32" and xd == "f32":
+                ref_check(got, want, REF_TOL)
+            else:
+                tier_check(got, want, TIER_F32_ACC)
+
+
+def test_static_entry_rejects_oversized_rows(hip):
+    """More rows of fp32 activations than the scratch holds shifts for: a clear error, no work."""
+    lib = _abi.load()
+    g = synth.rng(9950)
+    K, N = 64, 32
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    M = (16 << 20) // 4 + 1
+    rc = lib.byhip_q4_matmul_static(None, hip.F32, w.handle, None, hip.F32, M)
+    assert rc == _abi.BYHIP_ERROR
+    assert "at most 4194304 rows" in _abi.last_error()
