@@ -5,11 +5,15 @@
 
 Prints ONE JSON line. The headline (`value`) is config 1 of BASELINE.json: the decode Q4 GEMV
 (M=1, K=4096, N=14336, block-32 Q4 weights with fp16 scales, fp16 x and y, fp32 accumulation) in
-GB/s of algorithmic bytes, inputs resident in HBM. A step is one GEMV launch; K launches are
-recorded as one HIP graph (the session record / replay route) cycling through 17 resident copies of
-the weights (562 MB, more than twice the 256 MB Infinity Cache, so the reads come from HBM), and
-timed with HIP events on the library stream. The other configurations (prefill Q4 GEMM, MXFP4
-GEMM, the decoder-layer batch) are reported under "configs" with the same method.
+GB/s of algorithmic bytes, inputs resident in HBM. A step is one GEMV launch. Each measurement is
+one session recording (a HIP graph) of a lead-in (a full rotation of the resident weight copies,
+then the W warmup steps) followed by exactly K timed steps, with a timing mark before and after
+the K steps: a one-thread kernel storing the GPU's constant-rate realtime counter
+(byhip_session_mark). Before it, a settle phase replays the rotation for 200 ms of GPU time so the
+clocks have left idle. The GEMV cycles through 17 resident weight copies (562 MB, more than twice
+the 256 MB Infinity Cache), and the rotation continues across the phases, so every read comes from
+HBM. The other configurations (prefill Q4 GEMM, MXFP4 GEMM, the decoder-layer batch, the fused
+decode layer) are reported under "configs" with the same method.
 
 roofline.traffic: HBM bytes per launch of the GEMV, read from profiles/q4_gemv_c1_traffic.json,
 which bybylang_amd.profile_summary writes from two rocprofv3 --pmc runs of this script
@@ -19,8 +23,11 @@ absent.
 
 cpu_baseline: the reference's own CPU path for this op (nimf_cpu_matmul_q4,
 backends/cpu/cpu_kernels_impl.inc:293-319, compiled from its sources into oracle/_ref), single
-threaded as the reference runs, timed on full config-1 passes for about ten seconds; when that
-library is absent, the C restatement in oracle/ ("port").
+threaded as the reference runs, on full config-1 passes; when that library is absent, the C
+restatement in oracle/ ("port"). cpu_baselines: the same path on every configuration (the CPU VM's
+OP_TILE_GEMM for the FP4 one), on one core and on all the host's cores (at most 16, the box's
+share), splitting rows or columns over threads with bit-identical per-output loops; configs whose
+full run would take minutes time a stated row subset and scale linearly in M.
 """
 from __future__ import annotations
 
@@ -83,7 +90,7 @@ class Recorder:
         self.gb.sessionFreeRecording(self.gb.gbHip, self.id)
 
 
-SETTLE_MS = 100.0  # GPU time of untimed work before each timing, so the clocks are out of idle
+SETTLE_MS = 200.0  # GPU time of untimed work before each timing, so the clocks are out of idle
 # The timing marks are the library's events recorded inside the recording, around exactly the
 # timed steps (byhip_session_mark); without them (BENCH_MARKS=0) the lead-in and the timed steps are
 # two recordings queued back to back with events between them (byhip_session_replay_after).
@@ -338,6 +345,24 @@ def bench_c4_fused(dev, synth, steps, warmup):
     per = gpu_s / steps
     out.update({"batch_us": per * 1e6, "batch_GBps": layer_bytes / per / 1e9, "weight_copies": copies,
                 "launches": len(C4_FUSED)})
+
+    # The unfused sequence's GEMVs: the same seven matrices as plain fp32-in, fp32-out GEMVs (one
+    # launch each, the input of the norm-free form). Its RMSNorms, silu * up and residual adds (five
+    # more launches) are not kernels of this library and are not timed: this is a lower bound of
+    # the unfused layer.
+    ys = {(op[0], j): dev.DeviceBuffer(N * 4) for op in ops for j, N in enumerate(op[3])}
+
+    def unfused(i):
+        for name, mode, K, Ns, norm, res, mats, a, outs, gamma, r in ops:
+            for j, N in enumerate(Ns):
+                dev.q4_matmul(a, dev.F32, mats[j][i % copies], ys[(name, j)], dev.F32, 1)
+
+    gpu_s, _ = run_steps(unfused, steps, warmup, settle_steps=copies)
+    out["unfused_gemvs"] = {"us": gpu_s / steps * 1e6, "launches": sum(len(op[3]) for op in ops),
+                            "note": "7 plain fp32 GEMVs only; the unfused layer adds 2 RMSNorms, silu*up and "
+                                    "2 residual adds (5 launches) not timed here"}
+    for y in ys.values():
+        y.close()
     for op in ops:
         for m in op[6]:
             for w in m:
@@ -345,41 +370,169 @@ def bench_c4_fused(dev, synth, steps, warmup):
     return out
 
 
-def cpu_baseline(seconds: float = 10.0):
-    """The reference's single-threaded CPU Q4 matmul (or the oracle port) on full config-1 passes."""
-    from bybylang_amd import synth
-    ref = os.path.join(ROOT, "oracle", "_ref", "libbybyref.so")
-    port = os.path.join(ROOT, "oracle", "liboracle.so")
-    if os.path.exists(ref):
-        lib = C.CDLL(ref)
-        fn, kind = lib.refshim_matmul_q4, "reference"
-        fn.argtypes = [C.c_void_p] * 5 + [C.c_int] * 5
-        call = lambda a, w, s, z, c: fn(a, w, s, z, c, M, K, N, 32, K // 32)  # noqa: E731
-    elif os.path.exists(port):
-        lib = C.CDLL(port)
-        fn, kind = lib.orc_matmul_q4, "port"
-        fn.argtypes = [C.c_void_p] * 5 + [C.c_int] * 7
-        call = lambda a, w, s, z, c: fn(a, w, s, z, c, M, K, N, 32, K // 32, 0, M)  # noqa: E731
-    else:
-        return None
-    M, K, N = 1, 4096, 14336
-    g = synth.rng(1)
-    wq, sc, ze, _ = synth.q4_weights(g, N, K)
-    a = synth.activations(g, M, K, np.float16).astype(np.float32).reshape(-1)
-    c = np.zeros(M * N, np.float32)
-    ptrs = [v.ctypes.data for v in (a, wq, sc, ze, c)]
-    passes, t0 = 0, time.perf_counter()
+class CpuPath:
+    """The reference's CPU path for this op, timed on the host: its own C compiled from its sources
+    into oracle/_ref (kind "reference": nimf_cpu_matmul_q4 for Q4, the CPU VM's OP_TILE_GEMM for
+    FP4-KM), else the C restatement in oracle/ ("port"). The reference runs single-threaded; the
+    all-core figures split rows (or, at M = 1, columns) over threads, each thread running the
+    same per-output loops, so the outputs are bit-identical to one thread's."""
+
+    def __init__(self):
+        ref = os.path.join(ROOT, "oracle", "_ref", "libbybyref.so")
+        port = os.path.join(ROOT, "oracle", "liboracle.so")
+        if os.path.exists(ref):
+            self.lib, self.kind = C.CDLL(ref), "reference"
+            self.lib.refshim_matmul_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 5
+            self.lib.refshim_vm_run_slots.argtypes = ([C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                                                      C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                                      C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_int])
+        elif os.path.exists(port):
+            self.lib, self.kind = C.CDLL(port), "port"
+            self.lib.orc_matmul_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 7
+            self.lib.orc_tile_gemm.argtypes = ([C.c_uint32] * 4 + [C.c_uint64] * 2 +
+                                               [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p,
+                                                C.c_int64, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32,
+                                                C.c_char_p, C.c_int])
+        else:
+            raise FileNotFoundError("no CPU path built (oracle/_ref or oracle/liboracle.so)")
+
+    def q4(self, a, wq, sc, ze, c, M, K, N):
+        """Q4 group 32 on host pointers (a [M, K] fp32, rows of wq, fp32 scales / zeros, c [M, N])."""
+        if self.kind == "reference":
+            self.lib.refshim_matmul_q4(a, wq, sc, ze, c, M, K, N, 32, K // 32)
+        else:
+            self.lib.orc_matmul_q4(a, wq, sc, ze, c, M, K, N, 32, K // 32, 0, M)
+
+    def fp4(self, x, blob, blob_len, table, out, M, K, N):
+        """The FP4-KM tile GEMM (the c3 format) on M rows: the CPU VM running OP_TILE_GEMM."""
+        if self.kind == "reference":
+            code = np.array([0xB0, M, K, N, N * (K // 2), 0, 0x01], dtype=np.uint32)
+            err = C.create_string_buffer(256)
+            rc = self.lib.refshim_vm_run_slots(code.ctypes.data, code.size, out, M * N, blob, blob_len,
+                                               table, 272, x, M * K, 128, 64, 128, err, 256)
+        else:
+            err = C.create_string_buffer(256)
+            rc = self.lib.orc_tile_gemm(0, M, K, N, N * (K // 2), 0, blob, blob_len, table, 272, x, M * K,
+                                        out, M * N, 0, M, err, 256)
+        assert rc == 0, err.value
+
+
+def cpu_threads() -> int:
+    """Threads for the all-core figures: the host's cores, at most the box's CPU share (16, as
+    OMP_NUM_THREADS says there)."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, min(n, 16))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _timed(fn, min_seconds):
+    """Seconds per call of fn, over at least min_seconds (and at least one call)."""
+    calls, t0 = 0, time.perf_counter()
     while True:
-        call(*ptrs)
-        passes += 1
+        fn()
+        calls += 1
         el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    per = el / passes
-    return {"value": q4_bytes(M, K, N) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{passes} full config-1 passes (M=1 K=4096 N=14336, fp32 x) in {el:.1f} s, "
-                      f"{per * 1e3:.1f} ms each, nimf_cpu_matmul_q4 single thread on "
-                      f"{platform.processor() or platform.machine()}"}
+        if el >= min_seconds:
+            return el / calls
+
+
+def _parallel(jobs, threads):
+    """Runs the callables on `threads` threads (ctypes releases the GIL inside the C calls)."""
+    import concurrent.futures as cf
+    with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+        for f in [ex.submit(j) for j in jobs]:
+            f.result()
+
+
+def cpu_q4_case(cpu, M, K, N, rows, threads, min_s, seed):
+    """Seconds for all M rows of a Q4 product on 1 and on `threads` cores: `rows` rows timed (all
+    of them when rows >= M) and scaled by M / rows; at M = 1 the all-core run splits columns."""
+    from bybylang_amd import synth
+    g = synth.rng(seed)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    R = min(M, rows)
+    a = synth.activations(g, R, K, np.float32).reshape(-1)
+    c = np.zeros(R * N, np.float32)
+    P = lambda arr, off=0: int(arr.ctypes.data + int(off) * arr.itemsize)  # noqa: E731
+    one = _timed(lambda: cpu.q4(P(a), P(wq), P(sc), P(ze), P(c), R, K, N), min_s) * M / R
+    gpr = K // 32
+    if R == 1:  # columns split over the threads
+        cuts = np.linspace(0, N, threads + 1).astype(int)
+        jobs = [lambda n0=n0, n1=n1: cpu.q4(P(a), P(wq, n0 * (K // 2)), P(sc, n0 * gpr), P(ze, n0 * gpr), P(c, n0),
+                                            1, K, n1 - n0) for n0, n1 in zip(cuts[:-1], cuts[1:]) if n1 > n0]
+        allc = _timed(lambda: _parallel(jobs, threads), min_s) * M
+    else:  # rows over the threads: every thread its own row block
+        Ra = min(M, max(R, threads))
+        aa = synth.activations(g, Ra, K, np.float32).reshape(-1)
+        ca = np.zeros(Ra * N, np.float32)
+        cuts = np.linspace(0, Ra, threads + 1).astype(int)
+        jobs = [lambda r0=r0, r1=r1: cpu.q4(P(aa, r0 * K), P(wq), P(sc), P(ze), P(ca, r0 * N), r1 - r0, K, N)
+                for r0, r1 in zip(cuts[:-1], cuts[1:]) if r1 > r0]
+        allc = _timed(lambda: _parallel(jobs, threads), min_s) * M / Ra
+    return one, allc, R
+
+
+def cpu_baselines(threads: int, min_s: float = 0.8):
+    """The reference CPU path on every configuration, one core and `threads` cores."""
+    from bybylang_amd import synth
+    cpu = CpuPath()
+    out = {"kind": cpu.kind, "cpu_model": cpu_model(), "threads": threads, "nproc": os.cpu_count()}
+
+    def entry(one, allc, flops, nbytes, sample):
+        return {"s_1core": one, "s_all": allc, "GFLOPs_1core": flops / one / 1e9, "GFLOPs_all": flops / allc / 1e9,
+                "GBps_1core": nbytes / one / 1e9, "GBps_all": nbytes / allc / 1e9, "sample": sample}
+
+    for name, M, K, N, rows in (("c0", 16, 4096, 4096, 16), ("c1", 1, 4096, 14336, 1), ("c2", 512, 4096, 4096, 8)):
+        one, allc, R = cpu_q4_case(cpu, M, K, N, rows, threads, min_s, 60)
+        out[name] = entry(one, allc, 2 * M * K * N, q4_bytes(M, K, N),
+                          "full" if R >= M else f"{R} of {M} rows timed, scaled linearly in M")
+    # c3: the FP4-KM tile GEMM through the CPU VM, rows timed and scaled to M = 2048
+    M, K, N = 2048, 8192, 8192
+    g = synth.rng(63)
+    blob, _, _ = synth.mxfp4_operand(g, N, K)
+    table = synth.mx_table()
+    table[16 + 255] = 0.0
+    xs = synth.mx_decode(*synth.mxfp4_operand(g, threads, K)[1:]).reshape(-1)
+    o = np.zeros(threads * N, np.float32)
+    P = lambda arr, off=0: int(arr.ctypes.data + int(off) * arr.itemsize)  # noqa: E731
+    one = _timed(lambda: cpu.fp4(P(xs), P(blob), blob.size, P(table), P(o), 1, K, N), min_s) * M
+    jobs = [lambda r=r: cpu.fp4(P(xs, r * K), P(blob), blob.size, P(table), P(o, r * N), 1, K, N) for r in range(threads)]
+    allc = _timed(lambda: _parallel(jobs, threads), min_s) * M / threads
+    out["c3"] = entry(one, allc, 2 * M * K * N, mx_bytes(M, K, N),
+                      f"1 row (1 core) and {threads} rows ({threads} cores) of {M}, scaled linearly in M")
+    # c4: the four projections of the layer at M = 1, 32, 256
+    for M in (1, 32, 256):
+        one = allc = 0.0
+        for j, (_, K, N) in enumerate(C4_OPS):
+            o1, oa, _ = cpu_q4_case(cpu, M, K, N, 1, threads, min_s / 4, 70 + j)
+            one, allc = one + o1, allc + oa
+        flops = sum(2 * M * K * N for _, K, N in C4_OPS)
+        nbytes = sum(q4_bytes(M, K, N) for _, K, N in C4_OPS)
+        out[f"c4_M{M}"] = entry(one, allc, flops, nbytes,
+                                "full" if M == 1 else f"1 row per projection (all-core: {threads} rows), scaled to M = {M}")
+    return out
+
+
+def cpu_baseline(baselines):
+    """The headline's CPU figure: config 1 on one core, the reference's own single-threaded loops."""
+    c1 = baselines["c1"]
+    return {"value": c1["GBps_1core"], "unit": "GB/s", "cores": 1, "kind": baselines["kind"],
+            "sample": f"full config-1 passes (M=1 K=4096 N=14336, fp32 x), {c1['s_1core'] * 1e3:.1f} ms each, "
+                      f"nimf_cpu_matmul_q4 single thread on {baselines['cpu_model']}; on {baselines['threads']} "
+                      f"threads {c1['GBps_all']:.2f} GB/s"}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_c1_traffic.json")
@@ -441,7 +594,8 @@ def main() -> int:
     ap.add_argument("--configs", default="c1,c2,c3,c4,up,rp",
                     help="configurations to measure (c1 is the headline and always runs); c4t is c4 "
                          "with the batch timed again after byhip_q4_prepare tunes each projection")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=0.8,
+                    help="minimum seconds per CPU-baseline measurement (0: no CPU baseline)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run the copy kernel on MIB MiB (calibration for counter runs)")
     args = ap.parse_args()
@@ -472,7 +626,8 @@ def main() -> int:
         configs["resident_upload_mapped"] = bench_upload_mapped(synth)
     if "rp" in wanted:
         configs["hbm_read_probe"] = bench_read_probe(dev)
-    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    baselines = cpu_baselines(cpu_threads(), args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = cpu_baseline(baselines) if baselines else None
 
     per_s = c1["us_per_step"] * 1e-6
     line = {
@@ -491,7 +646,8 @@ def main() -> int:
         "config": {"workload": "c1 decode Q4 GEMV: M=1 K=4096 N=14336, block-32 Q4 + fp16 scales, "
                                "fp16 x/y, fp32 accumulate",
                    "weight_copies": c1["weight_copies"], "rotation_bytes": c1["rotation_bytes"],
-                   "timing": "one HIP-graph replay of `steps` launches, hipEvents on the library stream",
+                   "timing": "one recording (HIP graph): rotation lead-in, `warmup` steps, then `steps` timed "
+                             "launches between two realtime-counter marks; 200 ms settle before",
                    "device": info.get("name", ""), "arch": info.get("arch_name", ""),
                    "compute_units": info.get("compute_units")},
         "roofline": {"bound": "hbm", "achieved": round(c1["GBps"], 2), "peak": HBM_PEAK_GBS,
@@ -499,6 +655,7 @@ def main() -> int:
                      "traffic": measured_traffic(), "kernel": "q4_gemv",
                      "bytes_per_launch": c1["bytes_per_step"], "avg_launch_us": round(c1["us_per_step"], 3)},
         "cpu_baseline": cpu,
+        "cpu_baselines": baselines,
         "configs": configs,
     }
     if probe:
