@@ -550,10 +550,8 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 //   16-byte chunk c of row r at slot c ^ (r & 15): the fragment reads (16 rows, one chunk each)
 //   then hit 16 distinct bank groups. Each wave reads only what it loaded, so no barrier is
 //   needed; the double buffer and a vmcnt wait order the direct loads and the reads.
-//   Shapes: BM x 16 FN with FN = 4 column fragments for BM <= 32 (two blocks per CU), and the
-//   wide tile BM = 64, FN = 8 for prefill (one block per CU, 128 accumulators per lane): there
-//   each dequantized weight fragment feeds four row fragments and each activation fragment eight
-//   column fragments, so the dequantization VALU work and the LDS reads per MFMA both halve.
+//   Shapes: BM x 16 FN with FN = 4 column fragments and BM 16 or 32 (two blocks per CU). The
+//   64 x 128 prefill tile with the same operand layout is q4_gemm_wide.
 template <int FN>
 struct SkinnyW {
     v4u w[FN];       // 32 nibbles of one column per fragment
@@ -567,10 +565,9 @@ struct SkinnyLds {
     static constexpr int kBytes = kX > kRed ? kX : kRed;
 };
 
-constexpr int skinny_waves_per_simd(int BM, int FN) { return BM * FN > 128 ? 1 : 2; }
-
 template <int BM, int FN, int YT>
-__global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_skinny(GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
+    static_assert(FN <= 4 && BM <= 32, "q4_gemm_skinny: 16 or 32 rows, at most 4 column fragments");
     constexpr int FM = BM / 16, NV = FM * FN * 4;  // accumulator floats per lane
     constexpr int XDMA = BM / 4;                           // direct loads per step (4 rows each)
     constexpr int XBUF = BM * 256;                         // bytes of one activation buffer
@@ -614,12 +611,10 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
     const uint32_t sfrag = sblk ? 32u * G : 32u * (uint32_t)a.gpr;
     uint8_t* const xbuf = lds + wid * 2 * XBUF;
 
-    // Step t of this wave is block step (wid + 4t + rot) mod nsteps. For the narrow tiles the
-    // rotation by the block index staggers where blocks start along K; the wide tile keeps every
-    // block on the same K slice at about the same time, so the column blocks that share an
-    // activation slice find it in L2 (measured faster at prefill shapes).
+    // Step t of this wave is block step (wid + 4t + rot) mod nsteps: the rotation by the block
+    // index staggers where blocks start along K.
     const int nt = nsteps > wid ? (nsteps - wid + 3) / 4 : 0;
-    const int rot = nsteps > 0 && FN <= 4 ? (int)(blockIdx.x % (unsigned)nsteps) : 0;
+    const int rot = nsteps > 0 ? (int)(blockIdx.x % (unsigned)nsteps) : 0;
     auto kstep = [&](int t) {
         const int v = wid + 4 * t + rot;
         return v >= nsteps ? v - nsteps : v;
@@ -664,9 +659,8 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
             const _Float16 sc = bits_h((uint16_t)r.s[j]);
             ss[j] = (h2){sc, sc};
         }
-        // The step's activation fragments, read ahead of the math: all four MFMA columns (kk) up
-        // front when the block is narrow, two columns ahead when the wide tile needs the registers.
-        constexpr int XA = FN > 4 ? 2 : 4;
+        // The step's activation fragments for all four MFMA columns (kk), read ahead of the math.
+        constexpr int XA = 4;
         uint4 xv[XA][FM];
         auto xread = [&](int kk) {
 #pragma unroll
@@ -694,24 +688,13 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
                                            h2_bits((q2 - zz_lo) * ss[j]), h2_bits((q3 - zz_hi) * ss[j]));
                 bw[j] = *reinterpret_cast<const h8*>(&u);
             };
-            if constexpr (FN > 4) {
-                // wide tile: each weight fragment is dequantized just before its four MFMAs
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    dequant(j);
+            for (int j = 0; j < FN; ++j) dequant(j);
 #pragma unroll
-                    for (int i = 0; i < FM; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
-                }
-            } else {
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < FN; ++j) dequant(j);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
-            }
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
         }
     };
 
@@ -731,19 +714,10 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
         compute(cur, xcur);
         __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (FN > 4) {
-        // Two steps per iteration and no early exit: with 128 accumulators an early exit (or a
-        // single-step body) makes the register allocator move them between AGPRs every iteration.
-        for (int t = 0; t < nt; t += 2) {
-            step(t, ra, rb, xbuf, xbuf + XBUF);
-            step(t + 1, rb, ra, xbuf + XBUF, xbuf);
-        }
-    } else {
-        for (int t = 0; t < nt; t += 2) {
-            step(t, ra, rb, xbuf, xbuf + XBUF);
-            if (t + 1 >= nt) break;
-            step(t + 1, rb, ra, xbuf + XBUF, xbuf);
-        }
+    for (int t = 0; t < nt; t += 2) {
+        step(t, ra, rb, xbuf, xbuf + XBUF);
+        if (t + 1 >= nt) break;
+        step(t + 1, rb, ra, xbuf + XBUF, xbuf);
     }
 
     // Partial tiles of the four waves -> LDS (over the activation buffers, once every wave is done
@@ -768,6 +742,242 @@ __global__ __launch_bounds__(256, skinny_waves_per_simd(BM, FN)) void q4_gemm_sk
         if (m < a.M && n < a.N) {
             if (part) part[(size_t)m * a.N + n] = sum;
             else store_y<YT>(a.y, (size_t)m * a.N + n, sum);
+        }
+    }
+}
+
+// Wide Q4 GEMM for prefill shapes whose 64 x 128 tiles alone fill the CUs: q4_gemm_skinny's
+// layout (K steps dealt to groups of waves, partial tiles added at the end) with eight waves, two
+// per SIMD, so that one wave's MFMAs run while the other dequantizes (with one wave per SIMD the
+// dequantization VALU work beyond two instructions per MFMA leaves the MFMA pipe idle). Against
+// four waves of 64 x 128 each it took 25.3 us instead of 29.3 at M = 512, N = K = 4096, most of
+// it from the 16-byte output stores.
+//   Block: waves w and w + 4 (one SIMD) form group p = w % 4, which takes the block's K steps
+//   p, p + 4, ... (steps of 128); wave w of the group owns columns 64 h .. 64 h + 63 (h = w / 4)
+//   and all 64 rows, as 4 x 4 fragments of 16 x 16 (64 accumulators per lane).
+//   K order, weights and scales per lane as in q4_gemm_skinny: in MFMA kk lane group g supplies
+//   the values 32g + 8kk + (0, 4, 1, 5, 2, 6, 3, 7) of the step; a lane's weights for a step are
+//   one 16-byte load (one 32-value group) and one scale per fragment.
+//   Activations: the group's step slice (64 rows x 256 bytes) moves straight from global memory
+//   into one of the group's two LDS buffers, each wave of the group loading 32 rows, chunk c of
+//   row r at slot c ^ (r & 15). After a step's math every wave waits for its own loads of the
+//   next step, and one block barrier then publishes them and frees the buffer the loads after
+//   that overwrite. Every group runs ceil(steps / 4) steps, since the barrier needs the same
+//   count in every wave; a step past the group's last reads zeros and adds nothing.
+//   Output: the groups' partial tiles go to LDS in output layout (rows of 132 floats, so the
+//   accumulator writes hit 64 distinct banks), and each thread adds 8 neighbouring outputs in
+//   group order (0 + 1 + 2 + 3, the order of q4_gemm_skinny's wave sum) and writes them with
+//   16-byte stores.
+constexpr int kWideBM = 64, kWideBN = 128;
+constexpr int kWideXBuf = kWideBM * 256;                   // one activation buffer
+constexpr int kWidePitch = kWideBN + 4;                    // floats per row of a staged partial tile
+constexpr int kWideLdsX = 4 * 2 * kWideXBuf;               // 4 groups x 2 buffers
+constexpr int kWideLdsRed = 4 * kWideBM * kWidePitch * 4;  // 4 partial tiles
+constexpr int kWideLds = kWideLdsX > kWideLdsRed ? kWideLdsX : kWideLdsRed;
+
+template <int YT>
+__global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
+    constexpr int FM = 4, FN = 4;
+    constexpr int XDMA = 8;  // direct activation loads per wave and step (4 rows each)
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kWideLds];
+
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = wid & 3, h = wid >> 2;
+    const int c = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * kWideBN, m0 = blockIdx.y * kWideBM;
+    const int K = a.K;
+    const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
+    const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
+    const int nt_all = (nsteps + 3) / 4;                      // steps every group runs
+    const int nt = nsteps > p ? (nsteps - p + 3) / 4 : 0;     // the group's own steps
+
+    // Rows past M and columns past N read zeros through the range checks (the launcher keeps the
+    // offsets below 2^31).
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
+    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
+    const bool sblk = a.sblk != nullptr;
+    const uint32_t G = (uint32_t)K >> 5;
+    const rsrc_t sr = sblk ? make_rsrc(a.sblk, (uint32_t)(((size_t)a.N + 7) / 8 * 8 * G * 2))
+                           : make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
+    const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
+    // Direct load u (0..7) of wave h: rows 32h + 4u + lane / 16 of the tile, LDS slot lane % 16.
+    // Loads u and u + 4 differ by 16 rows and share the slot pattern.
+    uint32_t xo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 32 * h + 4 * q + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+        xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
+    }
+    const uint32_t xrow16 = 16u * (uint32_t)K * 2u;  // 16 activation rows
+    const int ncol = n0 + 64 * h + c;
+    const uint32_t wo = (uint32_t)ncol * (uint32_t)a.row_bytes + 16u * g;
+    const uint32_t so = sblk ? 2u * (((uint32_t)ncol >> 3) * G * 8u + 8u * g + (c & 7))
+                             : (uint32_t)ncol * (uint32_t)a.gpr;
+    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes;  // per fragment
+    const uint32_t sfrag = sblk ? 32u * G : 32u * (uint32_t)a.gpr;
+    uint8_t* const xgrp = lds + p * 2 * kWideXBuf;     // the group's two buffers
+
+    // The loads of step t of the group: XDMA direct activation loads into buffer `dst`, then FN
+    // weight and FN scale loads. A step past the group's last (t >= nt) adds 2^31 through the
+    // scalar offset, which every resource rejects: it reads zeros without touching memory.
+    auto load = [&](SkinnyW<FN>& r, uint8_t* __restrict__ dst, int t) {
+        const bool ok = t < nt;
+        const uint32_t k0 = (uint32_t)(s_first + (ok ? p + 4 * t : 0)) * 128u;
+        const uint32_t oob = ok ? 0u : 0x80000000u;
+        const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
+        const uint32_t soff = sblk ? so + 16u * (k0 >> 5) : 2u * (so + grp);
+#pragma unroll
+        for (int u = 0; u < XDMA; ++u)
+            lds_dma16(xr, dst + 1024 * (8 * h + u), xo[u & 3] + 2u * k0, oob + (uint32_t)(u >> 2) * xrow16);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 0);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, oob + (uint32_t)j * sfrag, 0);
+    };
+
+    const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
+    const h2 zz_lo = {zlo, zlo}, zz_hi = {zhi, zhi};
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
+
+    f4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const SkinnyW<FN>& r, const uint8_t* __restrict__ src) {
+        h2 ss[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const _Float16 sc = bits_h((uint16_t)r.s[j]);
+            ss[j] = (h2){sc, sc};
+        }
+        constexpr int XA = 2;  // activation columns read ahead
+        uint4 xv[XA][FM];
+        auto xread = [&](int kk) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                xv[kk % XA][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
+        };
+#pragma unroll
+        for (int kk = 0; kk < XA; ++kk) xread(kk);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            h8 bw[FN], ax[FM];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint4 u = perm8(xv[kk % XA][i]);
+                ax[i] = *reinterpret_cast<const h8*>(&u);
+            }
+            if (kk + XA < 4) xread(kk + XA);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint32_t d = r.w[j][kk], d8 = d >> 8;
+                const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
+                const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
+                const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
+                const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
+                const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss[j]), h2_bits((q1 - zz_hi) * ss[j]),
+                                           h2_bits((q2 - zz_lo) * ss[j]), h2_bits((q3 - zz_hi) * ss[j]));
+                bw[j] = *reinterpret_cast<const h8*>(&u);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Step t: issue the loads of step t + 1 (the other buffer and register set), compute step t,
+    // wait for this wave's loads, then the block barrier.
+    SkinnyW<FN> ra, rb;
+    load(ra, xgrp, 0);
+    wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    auto step = [&](int t, const SkinnyW<FN>& cur, SkinnyW<FN>& nxt, const uint8_t* __restrict__ xcur,
+                    uint8_t* __restrict__ xnxt) {
+        __builtin_amdgcn_sched_barrier(0);
+        load(nxt, xnxt, t + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(cur, xcur);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int t = 0; t < nt_all; t += 2) {
+        step(t, ra, rb, xgrp, xgrp + kWideXBuf);
+        if (t + 1 >= nt_all) break;  // uniform across the block
+        step(t + 1, rb, ra, xgrp + kWideXBuf, xgrp);
+    }
+
+    // Partial tiles -> LDS in output layout (every wave is past the last barrier, so the
+    // activation buffers are free) -> sums in group order -> y or the split-K partials.
+    float* red = reinterpret_cast<float*>(lds);  // [4 groups][64 rows][kWidePitch]
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[(p * kWideBM + 16 * i + 4 * g + r) * kWidePitch + 64 * h + 16 * j + c] = acc[i][j][r];
+    __syncthreads();
+    float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
+    constexpr int es = YT == BYHIP_F32 ? 4 : 2;
+    const bool wide_y = part ? a.N % 4 == 0 : ((uintptr_t)a.y % 16 == 0 && (size_t)a.N * es % 16 == 0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int u = (int)threadIdx.x + 512 * k;  // chunk of 8 outputs: row u / 16, columns 8 (u % 16)
+        const int row = u >> 4, col = (u & 15) * 8;
+        const int m = m0 + row, n = n0 + col;
+        float v[8];
+        const float* src = red + row * kWidePitch + col;
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            const float4 s0 = *reinterpret_cast<const float4*>(src + e);
+            const float4 s1 = *reinterpret_cast<const float4*>(src + kWideBM * kWidePitch + e);
+            const float4 s2 = *reinterpret_cast<const float4*>(src + 2 * kWideBM * kWidePitch + e);
+            const float4 s3 = *reinterpret_cast<const float4*>(src + 3 * kWideBM * kWidePitch + e);
+            v[e] = s0.x + s1.x + s2.x + s3.x;
+            v[e + 1] = s0.y + s1.y + s2.y + s3.y;
+            v[e + 2] = s0.z + s1.z + s2.z + s3.z;
+            v[e + 3] = s0.w + s1.w + s2.w + s3.w;
+        }
+        if (m >= a.M) continue;
+        if (wide_y && n + 8 <= a.N) {
+            if (part) {
+                float4* o = reinterpret_cast<float4*>(part + (size_t)m * a.N + n);
+                o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            } else if constexpr (YT == BYHIP_F32) {
+                float4* o = reinterpret_cast<float4*>(static_cast<float*>(a.y) + (size_t)m * a.N + n);
+                o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (YT == BYHIP_F16)
+                        w[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e]) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]) << 16);
+                    else
+                        w[e] = f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]);
+                }
+                *reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.y) + ((size_t)m * a.N + n) * es) =
+                    make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (n + e >= a.N) break;
+                if (part) part[(size_t)m * a.N + n + e] = v[e];
+                else store_y<YT>(a.y, (size_t)m * a.N + n + e, v[e]);
+            }
         }
     }
 }
@@ -990,6 +1200,16 @@ void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
     BYHIP_LAUNCHED("q4_gemm_skinny");
 }
 
+void launch_q4_wide(const GemmArgs& a, int splits) {
+    const dim3 grid((a.N + kWideBN - 1) / kWideBN, (a.M + kWideBM - 1) / kWideBM, splits);
+    switch (a.y_dtype) {
+    case BYHIP_F32: hipLaunchKernelGGL(q4_gemm_wide<BYHIP_F32>, grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL(q4_gemm_wide<BYHIP_F16>, grid, dim3(512), 0, stream(), a); break;
+    default: hipLaunchKernelGGL(q4_gemm_wide<BYHIP_BF16>, grid, dim3(512), 0, stream(), a); break;
+    }
+    BYHIP_LAUNCHED("q4_gemm_wide");
+}
+
 template <int BM, int BN>
 void launch_q4_pipe_shape(const GemmArgs& a, int splits) {
     const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
@@ -1094,13 +1314,13 @@ void launch_q4_big(const GemmArgs& a0, int split_choice = 0) {
 }
 
 // Rows per block: 16 or 32 (the smallest that holds M) with 64 columns and two blocks per CU, or
-// the wide 64 x 128 tile with one block per CU.
+// the wide 64 x 128 tile (q4_gemm_wide, eight waves) with one block per CU.
 void launch_q4_skinny(const GemmArgs& a0, int split_choice = 0, bool wide = false) {
     GemmArgs a = a0;
     const int bm = wide ? 64 : a.M <= 16 ? 16 : 32, cols = wide ? 128 : 64;
     const long tiles = (long)((a.N + cols - 1) / cols) * ((a.M + bm - 1) / bm);
     const int splits = choose_split(a, tiles, a.K / 128, 8, split_choice, wide ? 1 : 2);
-    if (wide) launch_q4_skinny_shape<64, 8>(a, splits);
+    if (wide) launch_q4_wide(a, splits);
     else if (bm == 16) launch_q4_skinny_shape<16, 4>(a, splits);
     else launch_q4_skinny_shape<32, 4>(a, splits);
     if (a.part) launch_splitk_sum(a, splits);

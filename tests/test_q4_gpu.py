@@ -206,9 +206,10 @@ def test_q4_gemm_skinny(hip, oracle, monkeypatch, M, splits, group):
 @pytest.mark.parametrize("group", [32, 128, 0])
 def test_q4_gemm_prefill_tiles(hip, oracle, monkeypatch, kind, shape, splits, group):
     """The prefill kernels (forced through BYHIP_Q4_PREFILL): the 128 x 256 tile (activations
-    shared through LDS, weights straight to MFMA registers) and the 64 x 128 skinny tile (K split
-    over the block's waves); ragged M and N, groups 32 / 128 / whole row, with and without split-K,
-    fp16 in and out, against the oracle; a repeat call is bit-identical."""
+    shared through LDS, weights straight to MFMA registers) and the 64 x 128 wide tile (K split
+    over four groups of two waves, 16-byte output stores); ragged M and N, groups 32 / 128 / whole
+    row, with and without split-K, fp16 in and out, against the oracle; a repeat call is
+    bit-identical."""
     from bybylang_amd import synth
     M, K, N = shape
     monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
