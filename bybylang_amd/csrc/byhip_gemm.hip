@@ -558,17 +558,62 @@ struct SkinnyW {
     uint32_t s[FN];  // their fp16 scale
 };
 
+// Partial tiles staged in LDS in output layout: rows of 16 FN + 4 floats, so that the accumulator
+// writes (lanes: 16 columns x 4 row groups) hit 64 distinct banks.
+constexpr int out_pitch(int FN) { return 16 * FN + 4; }
+
 template <int BM, int FN>
 struct SkinnyLds {
-    static constexpr int kX = 4 * 2 * BM * 256;               // 4 waves x 2 buffers x BM rows x 256 bytes
-    static constexpr int kRed = 4 * (BM / 16) * FN * 4 * 64 * 4;  // 4 partial tiles of the block
+    static constexpr int kX = 4 * 2 * BM * 256;                 // 4 waves x 2 buffers x BM rows x 256 bytes
+    static constexpr int kRed = 4 * BM * out_pitch(FN) * 4;      // 4 partial tiles of the block
     static constexpr int kBytes = kX > kRed ? kX : kRed;
 };
+
+// Whether 8-output chunks may leave as 16-byte stores: every row of y (or of the split-K
+// partials) starts 16-byte aligned.
+template <int YT>
+__device__ __forceinline__ bool out8_vector_ok(const GemmArgs& a, const float* part) {
+    constexpr int es = YT == BYHIP_F32 ? 4 : 2;
+    return part ? a.N % 4 == 0 : ((uintptr_t)a.y % 16 == 0 && (size_t)a.N * es % 16 == 0);
+}
+
+// Outputs v[0..7] of row m, columns n .. n + 7, to y (or to the split-K partials `part`): one
+// 16-byte store (fp16 / bf16) or two (fp32) when `vec` and all 8 columns exist, else one store per
+// column inside N.
+template <int YT>
+__device__ __forceinline__ void store_out8(const GemmArgs& a, float* part, bool vec, int m, int n, const float (&v)[8]) {
+    if (vec && n + 8 <= a.N) {
+        if (part || YT == BYHIP_F32) {
+            float* dst = part ? part + (size_t)m * a.N + n : static_cast<float*>(a.y) + (size_t)m * a.N + n;
+            reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+            reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (YT == BYHIP_F16)
+                    w[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e]) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]) << 16);
+                else
+                    w[e] = f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]);
+            }
+            *reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.y) + ((size_t)m * a.N + n) * 2) =
+                make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        if (n + e >= a.N) break;
+        if (part) part[(size_t)m * a.N + n + e] = v[e];
+        else store_y<YT>(a.y, (size_t)m * a.N + n + e, v[e]);
+    }
+}
 
 template <int BM, int FN, int YT>
 __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     static_assert(FN <= 4 && BM <= 32, "q4_gemm_skinny: 16 or 32 rows, at most 4 column fragments");
-    constexpr int FM = BM / 16, NV = FM * FN * 4;  // accumulator floats per lane
+    constexpr int FM = BM / 16;  // row fragments
     constexpr int XDMA = BM / 4;                           // direct loads per step (4 rows each)
     constexpr int XBUF = BM * 256;                         // bytes of one activation buffer
     __shared__ __attribute__((aligned(16))) uint8_t lds[SkinnyLds<BM, FN>::kBytes];
@@ -724,25 +769,34 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     // with them and every direct load has landed) -> sum in wave order -> y or the split-K partials.
     wait_vmcnt<0>();
     __syncthreads();
-    float* red = reinterpret_cast<float*>(lds);  // [4][NV][64]
+    constexpr int P = out_pitch(FN), TN = 16 * FN;
+    float* red = reinterpret_cast<float*>(lds);  // [4 waves][BM rows][P]
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) red[(wid * NV + (i * FN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+            for (int r = 0; r < 4; ++r) red[(wid * BM + 16 * i + 4 * g + r) * P + 16 * j + c] = acc[i][j][r];
     __syncthreads();
     float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
-    for (int e = threadIdx.x; e < NV * 64; e += 256) {
-        const int v = e >> 6, l = e & 63;
-        const float sum = red[(0 * NV + v) * 64 + l] + red[(1 * NV + v) * 64 + l] +
-                          red[(2 * NV + v) * 64 + l] + red[(3 * NV + v) * 64 + l];
-        const int i = v / (FN * 4), j = (v >> 2) % FN, r = v & 3;
-        const int m = m0 + 16 * i + 4 * (l >> 4) + r, n = n0 + 16 * j + (l & 15);
-        if (m < a.M && n < a.N) {
-            if (part) part[(size_t)m * a.N + n] = sum;
-            else store_y<YT>(a.y, (size_t)m * a.N + n, sum);
+    const bool vec = out8_vector_ok<YT>(a, part);
+    // chunk u of 8 outputs: row u / (TN / 8), columns 8 (u % (TN / 8))
+    for (int u = threadIdx.x; u < BM * TN / 8; u += 256) {
+        const int row = u / (TN / 8), col = (u % (TN / 8)) * 8;
+        const float* src = red + row * P + col;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            const float4 s0 = *reinterpret_cast<const float4*>(src + e);
+            const float4 s1 = *reinterpret_cast<const float4*>(src + BM * P + e);
+            const float4 s2 = *reinterpret_cast<const float4*>(src + 2 * BM * P + e);
+            const float4 s3 = *reinterpret_cast<const float4*>(src + 3 * BM * P + e);
+            v[e] = s0.x + s1.x + s2.x + s3.x;
+            v[e + 1] = s0.y + s1.y + s2.y + s3.y;
+            v[e + 2] = s0.z + s1.z + s2.z + s3.z;
+            v[e + 3] = s0.w + s1.w + s2.w + s3.w;
         }
+        if (m0 + row < a.M) store_out8<YT>(a, part, vec, m0 + row, n0 + col, v);
     }
 }
 
@@ -770,7 +824,7 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   16-byte stores.
 constexpr int kWideBM = 64, kWideBN = 128;
 constexpr int kWideXBuf = kWideBM * 256;                   // one activation buffer
-constexpr int kWidePitch = kWideBN + 4;                    // floats per row of a staged partial tile
+constexpr int kWidePitch = out_pitch(kWideBN / 16);        // floats per row of a staged partial tile
 constexpr int kWideLdsX = 4 * 2 * kWideXBuf;               // 4 groups x 2 buffers
 constexpr int kWideLdsRed = 4 * kWideBM * kWidePitch * 4;  // 4 partial tiles
 constexpr int kWideLds = kWideLdsX > kWideLdsRed ? kWideLdsX : kWideLdsRed;
@@ -928,8 +982,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
                 red[(p * kWideBM + 16 * i + 4 * g + r) * kWidePitch + 64 * h + 16 * j + c] = acc[i][j][r];
     __syncthreads();
     float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
-    constexpr int es = YT == BYHIP_F32 ? 4 : 2;
-    const bool wide_y = part ? a.N % 4 == 0 : ((uintptr_t)a.y % 16 == 0 && (size_t)a.N * es % 16 == 0);
+    const bool vec = out8_vector_ok<YT>(a, part);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int u = (int)threadIdx.x + 512 * k;  // chunk of 8 outputs: row u / 16, columns 8 (u % 16)
@@ -948,37 +1001,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             v[e + 2] = s0.z + s1.z + s2.z + s3.z;
             v[e + 3] = s0.w + s1.w + s2.w + s3.w;
         }
-        if (m >= a.M) continue;
-        if (wide_y && n + 8 <= a.N) {
-            if (part) {
-                float4* o = reinterpret_cast<float4*>(part + (size_t)m * a.N + n);
-                o[0] = make_float4(v[0], v[1], v[2], v[3]);
-                o[1] = make_float4(v[4], v[5], v[6], v[7]);
-            } else if constexpr (YT == BYHIP_F32) {
-                float4* o = reinterpret_cast<float4*>(static_cast<float*>(a.y) + (size_t)m * a.N + n);
-                o[0] = make_float4(v[0], v[1], v[2], v[3]);
-                o[1] = make_float4(v[4], v[5], v[6], v[7]);
-            } else {
-                uint32_t w[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (YT == BYHIP_F16)
-                        w[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e]) |
-                               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]) << 16);
-                    else
-                        w[e] = f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]);
-                }
-                *reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.y) + ((size_t)m * a.N + n) * es) =
-                    make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (n + e >= a.N) break;
-                if (part) part[(size_t)m * a.N + n + e] = v[e];
-                else store_y<YT>(a.y, (size_t)m * a.N + n + e, v[e]);
-            }
-        }
+        if (m < a.M) store_out8<YT>(a, part, vec, m, n, v);
     }
 }
 
@@ -1337,16 +1360,16 @@ int q4_big_splits(const GemmArgs& a) {
 
 // The Q4 prefill kernel (M above the skinny kernel's range) for the benchmark format, from
 // measurements on MI355X:
-//   the 64 x 128 wide skinny tile when its tiles alone fill the CUs while 128 x 256 tiles would
-//   leave more than half of them idle (M = 512, N = K = 4096: 34 us against 38 us);
+//   the 64 x 128 wide tile when its tiles alone fill the CUs while 128 x 256 tiles would leave
+//   more than half of them idle (M = 512, N = K = 4096: 25 us against 38 us);
 //   else, for M > 64, the 128 x 256 tile, which reads about half the operand bytes per output,
-//   unless the split-K it needs to fill the CUs would move more partial-sum bytes (8 per output
-//   and split: written, then read) than its tiles read operand bytes (400 per tile and K value);
-//   it wins on M = 256 gate+up (82 us against 130 us) and on the K = 14336 down projection, and
-//   loses with 8 splits of K = 4096 (M = 128 or 256, N = 4096), where the wide tile is used, as
-//   it is for M <= 64 (half-empty large tiles);
+//   unless the split-K it needs to fill the CUs moves partial sums (8 bytes per output and split:
+//   written, then read) of more than 100 bytes per tile and K value. At M = 256 it wins on
+//   gate+up (no split: 76 us against 103 us) and loses on down (K = 14336, 8 splits: 52.0 us
+//   against 47.4), o (N = K = 4096: 30.3 against 22.7) and qkv (34.0 against 34.5, even); the wide
+//   tile also takes M <= 64 (half-empty large tiles);
 //   the pipelined kernel where neither takes the call (K % 128 != 0, offsets past 2^31).
-// BYHIP_Q4_PREFILL forces one: 1 the pipelined kernel, 2 the large tile, 3 the wide skinny tile,
+// BYHIP_Q4_PREFILL forces one: 1 the pipelined kernel, 2 the large tile, 3 the wide tile,
 // when it takes the call. Returns kQ4Pipe / kQ4Big / kQ4Wide, or 0 for the general kernel.
 int q4_prefill_kind(const GemmArgs& a) {
     const int forced = env_int("BYHIP_Q4_PREFILL", 0);
@@ -1361,7 +1384,7 @@ int q4_prefill_kind(const GemmArgs& a) {
     if (big && (a.M > 64 || !wide)) {
         const double splits = q4_big_splits(a);
         const double partial = splits > 1 ? 8.0 * a.M * a.N * splits : 0.0;
-        if (!wide || partial <= 400.0 * big_tiles * a.K) return kQ4Big;
+        if (!wide || partial <= 100.0 * big_tiles * a.K) return kQ4Big;
     }
     if (wide) return kQ4Wide;
     return pipe ? kQ4Pipe : 0;
