@@ -1184,22 +1184,33 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
     if (t + 1 < nsteps) step(t + 1, r1, 1, r0, 0);
     wait_vmcnt<0>();
 
-    // Accumulator (i, j, r) of lane l: row 16i + 4(l / 16) + r, column 64w + 16j + l % 16.
+    // Output: accumulator (i, j, r) of lane l is row 16i + 4(l / 16) + r, column 64w + 16j + l % 16.
+    // Each wave stages its 64 columns in its own LDS area, 64 rows at a time in output layout,
+    // and writes 8 outputs per lane and store (16 bytes). The block barrier frees the activation
+    // buffers; after it each wave reads back only what it wrote.
+    __syncthreads();
+    constexpr int P = out_pitch(kBigFN);  // 68 floats
+    float* stage = reinterpret_cast<float*>(lds) + wid * 64 * P;
     float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
+    const bool vec = out8_vector_ok<YT>(a, part);
 #pragma unroll
-    for (int i = 0; i < kBigFM; ++i)
+    for (int half = 0; half < 2; ++half) {
 #pragma unroll
-        for (int j = 0; j < kBigFN; ++j) {
-            const int n = n0 + 64 * wid + 16 * j + c;
+        for (int i = 0; i < kBigFM / 2; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 16 * i + 4 * g + r;
-                if (m < a.M && n < a.N) {
-                    if (part) part[(size_t)m * a.N + n] = acc[i][j][r];
-                    else store_y<YT>(a.y, (size_t)m * a.N + n, acc[i][j][r]);
-                }
-            }
+            for (int j = 0; j < kBigFN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) stage[(16 * i + 4 * g + r) * P + 16 * j + c] = acc[4 * half + i][j][r];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int u = lane + 64 * q, row = u >> 3, col = (u & 7) * 8;  // chunk: 8 of the 64 columns
+            const float4 lo = *reinterpret_cast<const float4*>(stage + row * P + col);
+            const float4 hi = *reinterpret_cast<const float4*>(stage + row * P + col + 4);
+            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            const int m = m0 + 64 * half + row;
+            if (m < a.M) store_out8<YT>(a, part, vec, m, n0 + 64 * wid + col, v);
         }
+    }
 }
 
 // Whether the pipelined Q4 kernel takes these arguments.
