@@ -95,6 +95,37 @@ SETTLE_MS = 200.0  # GPU time of untimed work before each timing, so the clocks 
 # timed steps (byhip_session_mark); without them (BENCH_MARKS=0) the lead-in and the timed steps are
 # two recordings queued back to back with events between them (byhip_session_replay_after).
 MARKS_IN_RECORDING = os.environ.get("BENCH_MARKS", "1") != "0"
+# --eager: every step's kernels are launched directly (no recording, no replay), between the same
+# realtime-counter marks. For profiler runs: the host's launch gaps are then inside the timed
+# region, so the per-step figures are upper bounds; the kernel durations the profiler reports
+# are the kernels' own.
+EAGER = False
+
+
+def run_steps_eager(fn, steps, warmup, settle_steps=8):
+    """run_steps without recordings: the settle rotation is launched directly until SETTLE_MS of
+    wall time has passed, then the W warmup steps, then the timed steps between two marks."""
+    from bybylang_amd import _abi
+    gb = Recorder.gb_module()
+    lib = _abi.load()
+    end = time.perf_counter() + SETTLE_MS * 1e-3
+    while time.perf_counter() < end:
+        for i in range(settle_steps):
+            fn(i - settle_steps)
+        _abi.check(lib.byhip_synchronize(), "synchronize")
+    for i in range(warmup):
+        fn(i)
+    assert gb.sessionSetGpuTiming(gb.gbHip, True)
+    wall0 = time.perf_counter()
+    _abi.check(lib.byhip_session_mark(0), "mark")
+    for i in range(steps):
+        fn(warmup + i)
+    _abi.check(lib.byhip_session_mark(1), "mark")
+    _abi.check(lib.byhip_session_take_marks(), "marks")
+    wall = time.perf_counter() - wall0
+    gpu_s = gb.sessionGpuSeconds(gb.gbHip)
+    gb.sessionSetGpuTiming(gb.gbHip, False)
+    return gpu_s, wall
 
 
 def run_steps(fn, steps, warmup, settle_steps=8):
@@ -109,6 +140,8 @@ def run_steps(fn, steps, warmup, settle_steps=8):
     is timed: the lead-in lasts long enough for the host to queue the timed launch behind it, so
     the GPU never waits for the host inside the timed region, and the first timed step reads a copy
     last read a whole rotation earlier."""
+    if EAGER:
+        return run_steps_eager(fn, steps, warmup, settle_steps)
     from bybylang_amd import _abi
     gb = Recorder.gb_module()
     lib = _abi.load()
@@ -598,7 +631,11 @@ def main() -> int:
                     help="minimum seconds per CPU-baseline measurement (0: no CPU baseline)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run the copy kernel on MIB MiB (calibration for counter runs)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every step directly instead of replaying recordings (profiler runs)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.stderr.write("bench.py measures one GPU only: this build has no multi-GPU path "
                          "(collectives are out of scope); run with --gpus 1\n")
@@ -646,8 +683,11 @@ def main() -> int:
         "config": {"workload": "c1 decode Q4 GEMV: M=1 K=4096 N=14336, block-32 Q4 + fp16 scales, "
                                "fp16 x/y, fp32 accumulate",
                    "weight_copies": c1["weight_copies"], "rotation_bytes": c1["rotation_bytes"],
-                   "timing": "one recording (HIP graph): rotation lead-in, `warmup` steps, then `steps` timed "
-                             "launches between two realtime-counter marks; 200 ms settle before",
+                   "timing": ("eager launches (profiler run): 200 ms settle, `warmup` steps, then `steps` "
+                              "timed launches between two realtime-counter marks, host launch gaps included"
+                              if EAGER else
+                              "one recording (HIP graph): rotation lead-in, `warmup` steps, then `steps` timed "
+                              "launches between two realtime-counter marks; 200 ms settle before"),
                    "device": info.get("name", ""), "arch": info.get("arch_name", ""),
                    "compute_units": info.get("compute_units")},
         "roofline": {"bound": "hbm", "achieved": round(c1["GBps"], 2), "peak": HBM_PEAK_GBS,

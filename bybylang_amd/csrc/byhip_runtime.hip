@@ -562,15 +562,46 @@ int byhip_session_replay_after(int pre_id, int pre_times, int id, int times) {
     });
 }
 
+namespace {
+
+// Zeroes both mark slots on the library stream (outside recordings only: no copy is captured).
+void clear_marks(State& s) {
+    const unsigned long long unset[2] = {0, 0};
+    BYHIP_HIP(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_marks), unset, sizeof unset, 0, hipMemcpyHostToDevice, s.stream));
+}
+
+// Waits for the stream, reads both slots and counts end - begin (timing on); fails unless the
+// stream stored a begin and a later end since the slots were cleared.
+void take_marks(State& s, const char* what) {
+    unsigned long long t[2] = {0, 0};
+    BYHIP_HIP(hipMemcpyFromSymbolAsync(t, HIP_SYMBOL(g_marks), sizeof t, 0, hipMemcpyDeviceToHost, s.stream));
+    BYHIP_HIP(hipStreamSynchronize(s.stream));
+    if (!t[0] || !t[1] || t[1] < t[0]) fail("byhip: %s holds no pair of timing marks", what);
+    if (s.timing) s.gpu_seconds += (double)(t[1] - t[0]) / s.realtime_hz;
+}
+
+}  // namespace
+
 int byhip_session_mark(int which) {
     return guard([&] {
         enter_compute();
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
-        if (!s.recording) fail("byhip: a mark is recorded inside a recording");
         if (which != 0 && which != 1) fail("byhip: mark %d (0: begin, 1: end)", which);
+        if (!s.recording && s.session_open) fail("byhip: marks go into a recording or outside a session");
+        if (!s.recording && which == 0) clear_marks(s);
         hipLaunchKernelGGL(timing_mark, dim3(1), dim3(1), 0, s.stream, which);
         BYHIP_LAUNCHED("timing_mark");
+    });
+}
+
+int byhip_session_take_marks() {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        if (s.session_open) fail("byhip: marks are taken outside a session");
+        take_marks(s, "the stream");
     });
 }
 
@@ -581,14 +612,11 @@ int byhip_session_replay_marked(int id) {
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (s.session_open) fail("byhip: replay runs outside a session");
         if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id]) fail("byhip: no recording %d", id);
-        const unsigned long long unset[2] = {0, 0};
-        BYHIP_HIP(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_marks), unset, sizeof unset, 0, hipMemcpyHostToDevice, s.stream));
+        clear_marks(s);
         BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
-        unsigned long long t[2] = {0, 0};
-        BYHIP_HIP(hipMemcpyFromSymbolAsync(t, HIP_SYMBOL(g_marks), sizeof t, 0, hipMemcpyDeviceToHost, s.stream));
-        BYHIP_HIP(hipStreamSynchronize(s.stream));
-        if (!t[0] || !t[1] || t[1] < t[0]) fail("byhip: recording %d holds no pair of timing marks", id);
-        if (s.timing) s.gpu_seconds += (double)(t[1] - t[0]) / s.realtime_hz;
+        char what[48];
+        snprintf(what, sizeof what, "recording %d", id);
+        take_marks(s, what);
     });
 }
 

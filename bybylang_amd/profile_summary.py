@@ -1,7 +1,9 @@
 """Summaries of rocprofv3 result databases for the committed profiles.
 
-    python -m bybylang_amd.profile_summary trace DB
-        per-kernel dispatch count and average / min / max duration (kernel-trace runs)
+    python -m bybylang_amd.profile_summary trace DB [--between-marks]
+        per-kernel dispatch count and average / min / max duration (kernel-trace runs); with
+        --between-marks only the dispatches that start between the two dispatches of each pair of
+        timing marks (the library's timing_mark kernel: bench.py's timed steps)
 
     python -m bybylang_amd.profile_summary traffic --fetch DB --write DB --copy-bytes N
                                                    --kernel SUBSTRING [--json OUT]
@@ -32,6 +34,22 @@ def kernel_durations(db: str):
                        "from kernels group by name order by sum(end-start) desc").fetchall()
     con.close()
     return rows
+
+
+def kernel_durations_between_marks(db: str):
+    """kernel_durations over the dispatches that start between consecutive timing_mark dispatches
+    (pairs 1-2, 3-4, ...), in the same row format."""
+    con = sqlite3.connect(db)
+    rows = con.execute("select name, start, end from kernels order by start").fetchall()
+    con.close()
+    marks = [st for name, st, _ in rows if "timing_mark" in name]
+    spans = list(zip(marks[0::2], marks[1::2]))
+    per = collections.defaultdict(list)
+    for name, st, en in rows:
+        if "timing_mark" not in name and any(a < st < b for a, b in spans):
+            per[name].append(en - st)
+    out = [(k, len(v), sum(v) / len(v), min(v), max(v)) for k, v in per.items()]
+    return sorted(out, key=lambda r: -r[1] * r[2])
 
 
 def counter_per_dispatch(db: str, counter: str):
@@ -99,6 +117,7 @@ def main(argv=None) -> int:
     sub = ap.add_subparsers(dest="cmd", required=True)
     t = sub.add_parser("trace")
     t.add_argument("db")
+    t.add_argument("--between-marks", action="store_true")
     r = sub.add_parser("traffic")
     r.add_argument("--fetch", required=True)
     r.add_argument("--write", required=True)
@@ -117,7 +136,8 @@ def main(argv=None) -> int:
         return 0
     if a.cmd == "trace":
         print(f"| kernel | dispatches | avg us | min us | max us |\n|---|---:|---:|---:|---:|")
-        for name, n, avg, mn, mx in kernel_durations(a.db):
+        rows = kernel_durations_between_marks(a.db) if a.between_marks else kernel_durations(a.db)
+        for name, n, avg, mn, mx in rows:
             print(f"| `{name[:110]}` | {n} | {avg / 1e3:.3f} | {mn / 1e3:.3f} | {mx / 1e3:.3f} |")
         return 0
     res = traffic(a.fetch, a.write, a.copy_bytes, a.kernel)

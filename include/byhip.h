@@ -132,14 +132,17 @@ int byhip_session_replay(int id, int times);
  * counts only the latter in byhip_session_gpu_seconds(). All launches are queued before the one
  * wait, so the timed events never include the host's launch latency. */
 int byhip_session_replay_after(int pre_id, int pre_times, int id, int times);
-/* Measurement marks, with no counterpart in the reference: inside a recording,
- * byhip_session_mark(0) and (1) record a one-thread kernel that stores the GPU's constant-rate
- * realtime counter into the library's begin and end slots; byhip_session_replay_marked(id) launches
- * the recording once, waits, and counts the time between the two stores in
- * byhip_session_gpu_seconds() (timing on). The slots are the library's: one marked replay at a
- * time. */
+/* Measurement marks, with no counterpart in the reference: byhip_session_mark(0) and (1) launch
+ * (or, inside a recording, record) a one-thread kernel that stores the GPU's constant-rate
+ * realtime counter into the library's begin and end slots. byhip_session_replay_marked(id)
+ * launches a recording holding both marks once, waits, and counts the time between the two
+ * stores in byhip_session_gpu_seconds() (timing on). Outside recordings and sessions, mark(0)
+ * clears the slots before its kernel, and byhip_session_take_marks() waits for the stream and
+ * counts the same interval for directly launched work. The slots are the library's: one marked
+ * interval at a time. */
 int byhip_session_mark(int which);
 int byhip_session_replay_marked(int id);
+int byhip_session_take_marks(void);
 /* sessionFreeRecording. */
 int byhip_session_free_recording(int id);
 

@@ -177,3 +177,54 @@ def test_gpu_seconds(gb):
     for h in (ha, hc):
         gb.sessionFree(gb.gbHip, h)
     gb.residentFreeQ4(w)
+
+
+def test_timing_marks_direct_and_recorded(gb, hip):
+    """The measurement marks (no counterpart in the reference): work launched directly between
+    byhip_session_mark(0) and (1) is counted by byhip_session_take_marks, the same work recorded
+    between the two marks by byhip_session_replay_marked; an interval with no end mark and a
+    marked replay of a recording without marks are refused."""
+    lib = _abi.load()
+    g = synth.rng(9500)
+    K, N, n = 4096, 4096, 50
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    x = hip.DeviceBuffer.from_array(synth.activations(g, 1, K, np.float16).reshape(-1))
+    y = hip.DeviceBuffer(N * 2)
+    run = lambda: hip.q4_matmul(x, hip.F16, w, y, hip.F16, 1)  # noqa: E731
+    run()
+    assert gb.sessionSetGpuTiming(gb.gbHip, True)
+    _abi.check(lib.byhip_session_mark(0), "mark")
+    for _ in range(n):
+        run()
+    _abi.check(lib.byhip_session_mark(1), "mark")
+    _abi.check(lib.byhip_session_take_marks(), "marks")
+    t_direct = gb.sessionGpuSeconds(gb.gbHip)
+    # 50 launches of a ~33 MB GEMV: at least 50 x 4 us of kernel time, and well under a second
+    assert 50 * 4e-6 < t_direct < 1.0
+
+    assert gb.sessionBeginRecording(gb.gbHip)
+    _abi.check(lib.byhip_session_mark(0), "mark")
+    for _ in range(n):
+        run()
+    _abi.check(lib.byhip_session_mark(1), "mark")
+    assert gb.sessionEnd(gb.gbHip)
+    rid = gb.sessionLastRecording(gb.gbHip)
+    _abi.check(lib.byhip_session_replay_marked(rid), "replay")
+    t_rec = gb.sessionGpuSeconds(gb.gbHip) - t_direct
+    assert 50 * 4e-6 < t_rec < 1.0
+
+    _abi.check(lib.byhip_session_mark(0), "mark")
+    with pytest.raises(_abi.HipBackendError, match="no pair of timing marks"):
+        _abi.check(lib.byhip_session_take_marks(), "marks")
+    assert gb.sessionBeginRecording(gb.gbHip)
+    run()
+    assert gb.sessionEnd(gb.gbHip)
+    bare = gb.sessionLastRecording(gb.gbHip)
+    with pytest.raises(_abi.HipBackendError, match="no pair of timing marks"):
+        _abi.check(lib.byhip_session_replay_marked(bare), "replay")
+    assert gb.sessionSetGpuTiming(gb.gbHip, False)
+    for r in (rid, bare):
+        gb.sessionFreeRecording(gb.gbHip, r)
+    for b in (x, y, w):
+        b.close()
