@@ -33,6 +33,8 @@ struct GemmArgs {
     int gpr = 0;
     const void* sblk = nullptr;    // fp16 scales per 32-value chunk in blocks of 8 columns,
                                    // [ceil(N/8)][K/32][8] (byhip_q4w::sblk), or null
+    const uint8_t* wpf = nullptr;  // the prefill copy of the nibbles and its scales
+    const void* spf = nullptr;     // (byhip_q4w::wpf, spf), or null
     // FP4-KM
     const uint8_t* blob = nullptr;
     size_t scale_base = 0;

@@ -800,39 +800,51 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     }
 }
 
-// Wide Q4 GEMM for prefill shapes whose 64 x 128 tiles alone fill the CUs: q4_gemm_skinny's
-// layout (K steps dealt to groups of waves, partial tiles added at the end) with eight waves, two
-// per SIMD, so that one wave's MFMAs run while the other dequantizes (with one wave per SIMD the
-// dequantization VALU work beyond two instructions per MFMA leaves the MFMA pipe idle). Against
-// four waves of 64 x 128 each it took 25.3 us instead of 29.3 at M = 512, N = K = 4096, most of
-// it from the 16-byte output stores.
-//   Block: waves w and w + 4 (one SIMD) form group p = w % 4, which takes the block's K steps
-//   p, p + 4, ... (steps of 128); wave w of the group owns columns 64 h .. 64 h + 63 (h = w / 4)
-//   and all 64 rows, as 4 x 4 fragments of 16 x 16 (64 accumulators per lane).
-//   K order, weights and scales per lane as in q4_gemm_skinny: in MFMA kk lane group g supplies
-//   the values 32g + 8kk + (0, 4, 1, 5, 2, 6, 3, 7) of the step; a lane's weights for a step are
-//   one 16-byte load (one 32-value group) and one scale per fragment.
-//   Activations: the group's step slice (64 rows x 256 bytes) moves straight from global memory
-//   into one of the group's two LDS buffers, each wave of the group loading 32 rows, chunk c of
-//   row r at slot c ^ (r & 15). After a step's math every wave waits for its own loads of the
-//   next step, and one block barrier then publishes them and frees the buffer the loads after
-//   that overwrite. Every group runs ceil(steps / 4) steps, since the barrier needs the same
-//   count in every wave; a step past the group's last reads zeros and adds nothing.
+// Wide Q4 GEMM for prefill shapes whose 64 x 128 tiles alone fill the CUs, on the weights' prefill
+// copy (byhip_q4w::wpf, spf). Eight waves, two per SIMD, so that one wave's MFMAs run while the
+// other dequantizes (with one wave per SIMD the dequantization VALU work beyond two instructions
+// per MFMA leaves the MFMA pipe idle).
+//   Block: waves w and w + 4 (one SIMD) form group p = w % 4, which takes the block's K sub-steps
+//   p, p + 4, ... (64 values each); wave w of the group owns columns 64 h .. 64 h + 63 (h = w / 4)
+//   and all 64 rows, as 4 x 4 fragments of v_mfma_f32_16x16x32_f16 (64 accumulators per lane).
+//   K order: in MFMA kk (0, 1) of a sub-step, lane group g supplies the values 16 g + 8 kk .. + 7 in
+//   natural order, for the weights (the prefill copy's nibble order makes one AND-OR against the
+//   exponent words yield them so) and the activations alike: no permutation.
+//   Weights: per fragment and sub-step a lane's 16 nibbles are 8 contiguous bytes of a 512-byte
+//   block, so a load touches whole lines; its four fragments' scales are one 8-byte load.
+//   Activations: the group's sub-step slice (64 rows x 128 bytes, one line per row) moves straight
+//   from global memory into LDS, each wave of the group loading 32 rows, 16-byte chunk c of row r
+//   at slot c ^ ((r / 2) % 8): the fragment reads (16 rows, one chunk each) then hit 16 distinct
+//   bank groups. Four buffers per group: the loads of sub-step t + 3 are issued at sub-step t, so a
+//   sub-step's loads have three sub-steps of math to land in. At the start of each sub-step every
+//   wave waits for its own loads of it, and one block barrier publishes them and frees the buffer
+//   the next loads overwrite (read one sub-step earlier). Every group runs the same number of
+//   sub-steps, a multiple of four (the barrier needs the same count in every wave, and the loop
+//   body holds one sub-step per register set); a sub-step past the group's last reads zeros
+//   through an out-of-range offset and adds nothing.
 //   Output: the groups' partial tiles go to LDS in output layout (rows of 132 floats, so the
 //   accumulator writes hit 64 distinct banks), and each thread adds 8 neighbouring outputs in
-//   group order (0 + 1 + 2 + 3, the order of q4_gemm_skinny's wave sum) and writes them with
-//   16-byte stores.
+//   group order (0 + 1 + 2 + 3) and writes them with 16-byte stores.
 constexpr int kWideBM = 64, kWideBN = 128;
-constexpr int kWideXBuf = kWideBM * 256;                   // one activation buffer
+constexpr int kWideSub = 64;                               // K values per sub-step
+constexpr int kWideXBuf = kWideBM * kWideSub * 2;          // one activation buffer (8 KB)
+constexpr int kWideDepth = 4;                              // activation buffers per group
+constexpr int kWideLoads = 4 + 4 + 1;                      // loads per wave and sub-step
 constexpr int kWidePitch = out_pitch(kWideBN / 16);        // floats per row of a staged partial tile
-constexpr int kWideLdsX = 4 * 2 * kWideXBuf;               // 4 groups x 2 buffers
+constexpr int kWideLdsX = 4 * kWideDepth * kWideXBuf;      // 4 groups x 4 buffers
 constexpr int kWideLdsRed = 4 * kWideBM * kWidePitch * 4;  // 4 partial tiles
 constexpr int kWideLds = kWideLdsX > kWideLdsRed ? kWideLdsX : kWideLdsRed;
+
+// One wave's prefill-copy operands of one sub-step: per fragment 16 nibbles (two words), and the
+// four fragments' fp16 scales.
+struct WideW {
+    v2u w[4];
+    v2u s;
+};
 
 template <int YT>
 __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     constexpr int FM = 4, FN = 4;
-    constexpr int XDMA = 8;  // direct activation loads per wave and step (4 rows each)
     __shared__ __attribute__((aligned(16))) uint8_t lds[kWideLds];
 
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -840,55 +852,46 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     const int c = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * kWideBN, m0 = blockIdx.y * kWideBM;
     const int K = a.K;
+    const uint32_t nsub_all = (uint32_t)K / kWideSub;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
-    const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
-    const int nt_all = (nsteps + 3) / 4;                      // steps every group runs
-    const int nt = nsteps > p ? (nsteps - p + 3) / 4 : 0;     // the group's own steps
+    const int nsub = a.part ? min(a.split_steps, (int)nsub_all - s_first) : (int)nsub_all;  // the block's
+    const int nt_all = ((nsub + 3) / 4 + 3) & ~3;          // sub-steps every group runs (a multiple of 4)
+    const int nt = nsub > p ? (nsub - p + 3) / 4 : 0;     // the group's own sub-steps
 
     // Rows past M and columns past N read zeros through the range checks (the launcher keeps the
-    // offsets below 2^31).
+    // offsets below 2^31; the prefill copy pads N to whole fragments).
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
-    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
-    const bool sblk = a.sblk != nullptr;
-    const uint32_t G = (uint32_t)K >> 5;
-    const rsrc_t sr = sblk ? make_rsrc(a.sblk, (uint32_t)(((size_t)a.N + 7) / 8 * 8 * G * 2))
-                           : make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
-    const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
-    // Direct load u (0..7) of wave h: rows 32h + 4u + lane / 16 of the tile, LDS slot lane % 16.
-    // Loads u and u + 4 differ by 16 rows and share the slot pattern.
+    const rsrc_t wr = make_rsrc(a.wpf, (uint32_t)(((size_t)a.N + 15) / 16 * nsub_all * 512));
+    const rsrc_t sr = make_rsrc(a.spf, (uint32_t)(((size_t)a.N + 63) / 64 * nsub_all * 256));
+    // Direct load q (0..3) of wave h: rows 32 h + 8 q + lane / 8 of the tile, LDS slot lane % 8.
     uint32_t xo[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int r = 32 * h + 4 * q + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+        const int r = 32 * h + 8 * q + (lane >> 3), chunk = (lane & 7) ^ ((r >> 1) & 7);
         xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
-    const uint32_t xrow16 = 16u * (uint32_t)K * 2u;  // 16 activation rows
-    const int ncol = n0 + 64 * h + c;
-    const uint32_t wo = (uint32_t)ncol * (uint32_t)a.row_bytes + 16u * g;
-    const uint32_t so = sblk ? 2u * (((uint32_t)ncol >> 3) * G * 8u + 8u * g + (c & 7))
-                             : (uint32_t)ncol * (uint32_t)a.gpr;
-    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes;  // per fragment
-    const uint32_t sfrag = sblk ? 32u * G : 32u * (uint32_t)a.gpr;
-    uint8_t* const xgrp = lds + p * 2 * kWideXBuf;     // the group's two buffers
+    const uint32_t wfrag = nsub_all * 512u;  // per fragment
+    const uint32_t wo = (uint32_t)(n0 + 64 * h) / 16u * wfrag + 8u * lane;
+    const uint32_t so = (uint32_t)(n0 + 64 * h) / 64u * nsub_all * 256u + 8u * (16u * (uint32_t)(g >> 1) + c);
+    uint8_t* const xgrp = lds + p * kWideDepth * kWideXBuf;  // the group's buffers
+    // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot (2 g + kk) ^ (c / 2)
+    // ((16 i + c) / 2 % 8 is c / 2): one lane offset per kk, the fragment a constant 2048 i.
+    const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
 
-    // The loads of step t of the group: XDMA direct activation loads into buffer `dst`, then FN
-    // weight and FN scale loads. A step past the group's last (t >= nt) adds 2^31 through the
-    // scalar offset, which every resource rejects: it reads zeros without touching memory.
-    auto load = [&](SkinnyW<FN>& r, uint8_t* __restrict__ dst, int t) {
+    // The loads of the group's sub-step t (block sub-step p + 4 t) into buffer t % 4. A sub-step past
+    // the group's last (t >= nt) adds 2^31 through the scalar offset, which every resource rejects:
+    // it reads zeros without touching memory, and every sub-step issues the same loads.
+    auto load = [&](WideW& r, int t) {
         const bool ok = t < nt;
-        const uint32_t k0 = (uint32_t)(s_first + (ok ? p + 4 * t : 0)) * 128u;
+        const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
-        const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
-        const uint32_t soff = sblk ? so + 16u * (k0 >> 5) : 2u * (so + grp);
+        uint8_t* const dst = xgrp + (t & 3) * kWideXBuf;
 #pragma unroll
-        for (int u = 0; u < XDMA; ++u)
-            lds_dma16(xr, dst + 1024 * (8 * h + u), xo[u & 3] + 2u * k0, oob + (uint32_t)(u >> 2) * xrow16);
+        for (int q = 0; q < 4; ++q) lds_dma16(xr, dst + 1024 * (4 * h + q), xo[q] + 128u * u, oob);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-            r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 0);
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, oob + (uint32_t)j * sfrag, 0);
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + 512u * u, oob + (uint32_t)j * wfrag, 0);
+        r.s = __builtin_amdgcn_raw_buffer_load_b64(sr, so + 256u * u, oob, 0);
     };
 
     const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
@@ -903,31 +906,18 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const SkinnyW<FN>& r, const uint8_t* __restrict__ src) {
+    auto compute = [&](const WideW& r, const uint8_t* __restrict__ src) {
         h2 ss[FN];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const _Float16 sc = bits_h((uint16_t)r.s[j]);
+            const _Float16 sc = bits_h((uint16_t)(r.s[j >> 1] >> (16 * (j & 1))));
             ss[j] = (h2){sc, sc};
         }
-        constexpr int XA = 2;  // activation columns read ahead
-        uint4 xv[XA][FM];
-        auto xread = [&](int kk) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
-                xv[kk % XA][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
-        };
+        for (int kk = 0; kk < 2; ++kk) {
+            h8 ax[FM], bw[FN];
 #pragma unroll
-        for (int kk = 0; kk < XA; ++kk) xread(kk);
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            h8 bw[FN], ax[FM];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const uint4 u = perm8(xv[kk % XA][i]);
-                ax[i] = *reinterpret_cast<const h8*>(&u);
-            }
-            if (kk + XA < 4) xread(kk + XA);
+            for (int i = 0; i < FM; ++i) ax[i] = *reinterpret_cast<const h8*>(src + 2048 * i + (kk ? rd1 : rd0));
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const uint32_t d = r.w[j][kk], d8 = d >> 8;
@@ -947,31 +937,36 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         }
     };
 
-    // Step t: issue the loads of step t + 1 (the other buffer and register set), compute step t,
-    // wait for this wave's loads, then the block barrier.
-    SkinnyW<FN> ra, rb;
-    load(ra, xgrp, 0);
-    wait_vmcnt<0>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    auto step = [&](int t, const SkinnyW<FN>& cur, SkinnyW<FN>& nxt, const uint8_t* __restrict__ xcur,
-                    uint8_t* __restrict__ xnxt) {
+    // Sub-step t: wait for this wave's loads of t (those of t + 1 and t + 2 stay in flight), the
+    // barrier, the loads of t + 3 into the buffer t - 1 used, the math. Register sets rotate by four.
+    WideW r0, r1, r2, r3;
+    load(r0, 0);
+    load(r1, 1);
+    load(r2, 2);
+    auto step = [&](int t, const WideW& cur, WideW& nxt3) {
         __builtin_amdgcn_sched_barrier(0);
-        load(nxt, xnxt, t + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(cur, xcur);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<0>();
+        wait_vmcnt<2 * kWideLoads>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+        load(nxt3, t + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(cur, xgrp + (t & 3) * kWideXBuf);
+        __builtin_amdgcn_sched_barrier(0);
     };
-    for (int t = 0; t < nt_all; t += 2) {
-        step(t, ra, rb, xgrp, xgrp + kWideXBuf);
-        if (t + 1 >= nt_all) break;  // uniform across the block
-        step(t + 1, rb, ra, xgrp + kWideXBuf, xgrp);
+    // Four sub-steps per iteration and no early exit (an exit between them made the register
+    // allocator keep extra copies of the accumulators and spill).
+    for (int t = 0; t < nt_all; t += 4) {
+        step(t, r0, r3);
+        step(t + 1, r1, r0);
+        step(t + 2, r2, r1);
+        step(t + 3, r3, r2);
     }
 
-    // Partial tiles -> LDS in output layout (every wave is past the last barrier, so the
-    // activation buffers are free) -> sums in group order -> y or the split-K partials.
+    // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
+    // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
+    // group order -> y or the split-K partials.
+    wait_vmcnt<0>();
+    __syncthreads();
     float* red = reinterpret_cast<float*>(lds);  // [4 groups][64 rows][kWidePitch]
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -1313,11 +1308,12 @@ bool q4_skinny_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 64) * a.gpr * 2 < kLim;
 }
 
-// Whether the wide tile (64 x 128) takes the call: the pipelined kernel's conditions, K % 128 == 0
-// and all operand offsets, including the rows and columns a tile reaches past M and N, below 2^31.
+// Whether the wide tile (64 x 128) takes the call: the weights' prefill copy, the pipelined
+// kernel's conditions, K % 128 == 0 and all operand offsets, including the rows and columns a tile
+// reaches past M and N, below 2^31.
 bool q4_wide_ok(const GemmArgs& a) {
     constexpr uint64_t kLim = 0x80000000u;
-    return a.K % 128 == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + 64) * a.K * 2 < kLim &&
+    return a.wpf && a.spf && a.K % 128 == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + 64) * a.K * 2 < kLim &&
            (uint64_t)(a.N + 128) * a.row_bytes < kLim && (uint64_t)(a.N + 128) * a.gpr * 2 < kLim;
 }
 
@@ -1353,7 +1349,14 @@ void launch_q4_skinny(const GemmArgs& a0, int split_choice = 0, bool wide = fals
     GemmArgs a = a0;
     const int bm = wide ? 64 : a.M <= 16 ? 16 : 32, cols = wide ? 128 : 64;
     const long tiles = (long)((a.N + cols - 1) / cols) * ((a.M + bm - 1) / bm);
-    const int splits = choose_split(a, tiles, a.K / 128, 8, split_choice, wide ? 1 : 2);
+    // the wide kernel counts 64-value sub-steps, the skinny one 128-value steps
+    int splits = wide ? choose_split(a, tiles, a.K / kWideSub, 16, split_choice, 1)
+                      : choose_split(a, tiles, a.K / 128, 8, split_choice, 2);
+    if (wide && a.part) {
+        // slices of whole rounds of the wide kernel's loop: 4 groups x 4 sub-steps
+        a.split_steps = (a.split_steps + 15) / 16 * 16;
+        splits = (a.K / kWideSub + a.split_steps - 1) / a.split_steps;
+    }
     if (wide) launch_q4_wide(a, splits);
     else if (bm == 16) launch_q4_skinny_shape<16, 4>(a, splits);
     else launch_q4_skinny_shape<32, 4>(a, splits);

@@ -122,4 +122,14 @@ struct byhip_q4w {
     // these weights (rounding each product once); else the exact fp32 route runs them. Weights
     // built from micro-VM slots are not classified (0).
     int f16_safe = 0;
+    // Prefill copy, in the order the wide prefill kernel's lanes load it, built when the weights
+    // are fp16-safe with fp16 scales, one uniform zero, K % 64 == 0 and groups of a multiple of 32
+    // (or one per row); null otherwise. Per 16-column fragment f and 64-value K sub-step u, 512
+    // contiguous bytes: lane l = c + 16 g holds column 16 f + c, K positions 64 u + 16 g .. + 15 as
+    // two words, each holding positions 0..7 of its 8 as nibbles (0, 2, 4, 6, 1, 3, 5, 7) from bit 0,
+    // so that one AND-OR against the fp16 exponent words yields them in natural order. Scales: per
+    // 64 columns and sub-step, [2][16][4] fp16: the scales of columns 16 j + c (j = 0..3) for K
+    // positions 64 u + 32 t (t = g / 2), 8 bytes per lane.
+    uint8_t* wpf = nullptr;     // [ceil(N/16)][K/64][64][8]
+    void* spf = nullptr;        // [ceil(N/64)][K/64][2][16][4] fp16
 };

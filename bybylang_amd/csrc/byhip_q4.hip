@@ -160,6 +160,38 @@ __global__ __launch_bounds__(256) void q4_pack_scales(const float* __restrict__ 
     }
 }
 
+// The prefill copy (byhip_q4w::wpf, spf) from the nibble rows already on the device and the fp32
+// scales [N * gpr]: word i of wpf holds, for fragment f, sub-step u, lane l = c + 16 g and half d,
+// the nibbles of column 16 f + c at K positions p0 .. p0 + 7 (p0 = 64 u + 16 g + 8 d), position
+// p0 + k at bits 4 (k / 2) for even k and 16 + 4 (k / 2) for odd k; half i of spf the scale of
+// column 64 q + 16 j + c at K position 64 u + 32 t. Columns past N are zeros.
+__global__ __launch_bounds__(256) void q4_pack_prefill(const uint8_t* __restrict__ wq, size_t row_bytes,
+                                                       const float* __restrict__ sc, int N, int K, int gpr,
+                                                       int group, uint32_t* __restrict__ wpf,
+                                                       _Float16* __restrict__ spf) {
+    const size_t nsub = (size_t)K / 64;
+    const size_t nw = (size_t)(N + 15) / 16 * nsub * 128, ns = (size_t)(N + 63) / 64 * nsub * 128;
+    const size_t total = nw > ns ? nw : ns;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        if (i < nw) {
+            const size_t d = i & 1, l = (i >> 1) & 63, u = (i >> 7) % nsub, f = (i >> 7) / nsub;
+            const size_t n = 16 * f + (l & 15), p0 = 64 * u + 16 * (l >> 4) + 8 * d;
+            uint32_t v = 0;
+            if (n < (size_t)N) {
+                const uint32_t b = *reinterpret_cast<const uint32_t*>(wq + n * row_bytes + p0 / 2);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v |= ((b >> (4 * k)) & 15u) << ((k & 1) ? 16 + 4 * (k >> 1) : 4 * (k >> 1));
+            }
+            wpf[i] = v;
+        }
+        if (i < ns) {
+            const size_t j = i & 3, c = (i >> 2) & 15, t = (i >> 6) & 1, u = (i >> 7) % nsub, q = (i >> 7) / nsub;
+            const size_t n = 64 * q + 16 * j + c, p = 64 * u + 32 * t;
+            spf[i] = n < (size_t)N ? (_Float16)sc[n * gpr + (group ? p / (size_t)group : 0)] : (_Float16)0.0f;
+        }
+    }
+}
+
 // ── host side ───────────────────────────────────────────────────────────────────────────────
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -227,8 +259,14 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
     const size_t G = (size_t)K / 32, n_pad = ((size_t)N + 7) / 8 * 8;
     const size_t sb_bytes = blk ? n_pad * G * (sf16 ? 2 : 4) : 0;
     const size_t zb_bytes = blk && !zu ? n_pad * G * 4 : 0;
+    // Prefill copy (byhip_q4w::wpf, spf) for the fp16 MFMA prefill kernels.
+    const bool pf = f16_safe && sf16 && zu && K % 64 == 0 && (group == 0 || group % 32 == 0) && row_bytes % 4 == 0;
+    const size_t nsub = (size_t)K / 64;
+    const size_t wpf_bytes = pf ? ((size_t)N + 15) / 16 * nsub * 512 : 0;
+    const size_t spf_bytes = pf ? ((size_t)N + 63) / 64 * nsub * 256 : 0;
     const size_t o_s = align256(wq_bytes), o_z = o_s + align256(s_bytes), o_sb = o_z + align256(z_bytes),
-                 o_zb = o_sb + align256(sb_bytes), total = o_zb + align256(zb_bytes);
+                 o_zb = o_sb + align256(sb_bytes), o_wpf = o_zb + align256(zb_bytes),
+                 o_spf = o_wpf + align256(wpf_bytes), total = o_spf + align256(spf_bytes);
     uint8_t* base = static_cast<uint8_t*>(device_alloc(total));
     byhip_q4w* w = new byhip_q4w{};
     w->K = K; w->N = N; w->group = group; w->gpr = gpr; w->row_bytes = row_bytes;
@@ -243,6 +281,8 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
     w->zblk = blk && !zu ? reinterpret_cast<float*>(base + o_zb) : nullptr;
     w->blk_scale_f16 = sf16;
     w->f16_safe = f16_safe;
+    w->wpf = pf ? base + o_wpf : nullptr;
+    w->spf = pf ? base + o_spf : nullptr;
     try {
         BYHIP_HIP(hipMemcpyAsync(w->wq, wq_src, wq_bytes, wq_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                                  stream()));
@@ -251,6 +291,13 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
         hipLaunchKernelGGL(q4_pack_scales, dim3(pblocks), dim3(256), 0, stream(), d_sc, d_ze, N, gpr, group, (int)G,
                            (int)sf16, (int)zu, w->scales, w->zeros, w->sblk, w->zblk);
         BYHIP_LAUNCHED("q4_pack_scales");
+        if (pf) {
+            const size_t pw = std::max(((size_t)N + 15) / 16 * nsub * 128, ((size_t)N + 63) / 64 * nsub * 128);
+            const int fblocks = (int)std::min<size_t>((pw + 255) / 256, (size_t)compute_units() * 16);
+            hipLaunchKernelGGL(q4_pack_prefill, dim3(fblocks), dim3(256), 0, stream(), w->wq, row_bytes, d_sc, N, K,
+                               gpr, group, reinterpret_cast<uint32_t*>(w->wpf), static_cast<_Float16*>(w->spf));
+            BYHIP_LAUNCHED("q4_pack_prefill");
+        }
         BYHIP_HIP(hipStreamSynchronize(stream()));  // the source may be pageable host memory
     } catch (...) {
         device_free(base);
@@ -336,6 +383,8 @@ GemmArgs q4_gemm_args(const void* x, int x_dtype, const byhip_q4w* w, void* y, i
     a.wq = w->wq; a.row_bytes = w->row_bytes; a.scales = w->scales; a.scale_f16 = w->scale_f16;
     a.zeros = w->zeros; a.zero_value = w->zero_value; a.group = w->group; a.gpr = w->gpr;
     a.sblk = w->blk_scale_f16 ? w->sblk : nullptr;
+    a.wpf = w->wpf;
+    a.spf = w->spf;
     return a;
 }
 

@@ -200,8 +200,9 @@ def test_timing_marks_direct_and_recorded(gb, hip):
     _abi.check(lib.byhip_session_mark(1), "mark")
     _abi.check(lib.byhip_session_take_marks(), "marks")
     t_direct = gb.sessionGpuSeconds(gb.gbHip)
-    # 50 launches of a ~33 MB GEMV: at least 50 x 4 us of kernel time, and well under a second
-    assert 50 * 4e-6 < t_direct < 1.0
+    # 50 launches of a 33 MB GEMV (the weights stay in the 256 MB Infinity Cache between them): at
+    # least 1 us each even from there, and well under a second in all
+    assert 50 * 1e-6 < t_direct < 1.0
 
     assert gb.sessionBeginRecording(gb.gbHip)
     _abi.check(lib.byhip_session_mark(0), "mark")
@@ -212,7 +213,7 @@ def test_timing_marks_direct_and_recorded(gb, hip):
     rid = gb.sessionLastRecording(gb.gbHip)
     _abi.check(lib.byhip_session_replay_marked(rid), "replay")
     t_rec = gb.sessionGpuSeconds(gb.gbHip) - t_direct
-    assert 50 * 4e-6 < t_rec < 1.0
+    assert 50 * 1e-6 < t_rec < 1.0
 
     _abi.check(lib.byhip_session_mark(0), "mark")
     with pytest.raises(_abi.HipBackendError, match="no pair of timing marks"):
