@@ -801,9 +801,7 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 }
 
 // Wide Q4 GEMM for prefill shapes whose 64 x 128 tiles alone fill the CUs, on the weights' prefill
-// copy (byhip_q4w::wpf, spf). Eight waves, two per SIMD, so that one wave's MFMAs run while the
-// other dequantizes (with one wave per SIMD the dequantization VALU work beyond two instructions
-// per MFMA leaves the MFMA pipe idle).
+// copy (byhip_q4w::wpf, spf). Eight waves, two per SIMD.
 //   Block: waves w and w + 4 (one SIMD) form group p = w % 4, which takes the block's K sub-steps
 //   p, p + 4, ... (64 values each); wave w of the group owns columns 64 h .. 64 h + 63 (h = w / 4)
 //   and all 64 rows, as 4 x 4 fragments of v_mfma_f32_16x16x32_f16 (64 accumulators per lane).
@@ -815,13 +813,22 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   Activations: the group's sub-step slice (64 rows x 128 bytes, one line per row) moves straight
 //   from global memory into LDS, each wave of the group loading 32 rows, 16-byte chunk c of row r
 //   at slot c ^ ((r / 2) % 8): the fragment reads (16 rows, one chunk each) then hit 16 distinct
-//   bank groups. Four buffers per group: the loads of sub-step t + 3 are issued at sub-step t, so a
-//   sub-step's loads have three sub-steps of math to land in. At the start of each sub-step every
-//   wave waits for its own loads of it, and one block barrier publishes them and frees the buffer
-//   the next loads overwrite (read one sub-step earlier). Every group runs the same number of
-//   sub-steps, a multiple of four (the barrier needs the same count in every wave, and the loop
-//   body holds one sub-step per register set); a sub-step past the group's last reads zeros
-//   through an out-of-range offset and adds nothing.
+//   bank groups. Four buffers per group.
+//   Sub-step t of a group runs in two halves around one block barrier: the kk = 0 MFMAs beside
+//   the dequantization of the kk = 1 weights; the wait for this wave's loads of t + 1 and the
+//   barrier (which publishes every wave's direct loads of t + 1 and, since each wave's fragment
+//   reads of t have returned, frees buffer t % 4); the kk = 1 MFMAs beside the fragment reads of
+//   t + 1, the dequantization of t + 1's kk = 0 weights and the loads of t + 4 into buffer t % 4
+//   and the register set t just finished with. The dequantization VALU work thus runs between
+//   MFMAs of the same wave (interleaved by scheduling groups), and loads have three and a half
+//   sub-steps to land. Every group runs the same number of sub-steps, a multiple of four (the
+//   barrier needs the same count in every wave, and the loop body holds one sub-step per register
+//   set); a sub-step past the group's last reads zeros through an out-of-range offset and adds
+//   nothing. The last four sub-steps issue no loads (their waits count down instead).
+//   Tile order: with the tile count a multiple of 8, the workgroups that share an XCD (every 8th
+//   workgroup id) take a contiguous run of tiles in groups of 4 row tiles, so each XCD's L2 holds
+//   the activations of 4 row tiles and the weights of the column tiles it needs, rather than
+//   every row tile's activations.
 //   Output: the groups' partial tiles go to LDS in output layout (rows of 132 floats, so the
 //   accumulator writes hit 64 distinct banks), and each thread adds 8 neighbouring outputs in
 //   group order (0 + 1 + 2 + 3) and writes them with 16-byte stores.
@@ -842,6 +849,14 @@ struct WideW {
     v2u s;
 };
 
+// A sub-step's kind: whether it issues loads, and how many of this wave's loads may stay in flight
+// at its mid-step wait.
+template <bool L, int W>
+struct WideStep {
+    static constexpr bool load = L;
+    static constexpr int wait = W;
+};
+
 template <int YT>
 __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     constexpr int FM = 4, FN = 4;
@@ -850,7 +865,15 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = wid & 3, h = wid >> 2;
     const int c = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * kWideBN, m0 = blockIdx.y * kWideBM;
+    int bx = blockIdx.x, by = blockIdx.y;
+    {
+        const int gx = gridDim.x, gy = gridDim.y, tiles = gx * gy, id = bx + gx * by;
+        const int j = tiles % 8 == 0 ? (id % 8) * (tiles / 8) + id / 8 : id;
+        const int grp = j / (4 * gx), rows = min(4, gy - 4 * grp), r = j % (4 * gx);
+        by = 4 * grp + r % rows;
+        bx = r / rows;
+    }
+    const int n0 = bx * kWideBN, m0 = by * kWideBM;
     const int K = a.K;
     const uint32_t nsub_all = (uint32_t)K / kWideSub;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
@@ -878,20 +901,20 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // ((16 i + c) / 2 % 8 is c / 2): one lane offset per kk, the fragment a constant 2048 i.
     const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
 
-    // The loads of the group's sub-step t (block sub-step p + 4 t) into buffer t % 4. A sub-step past
-    // the group's last (t >= nt) adds 2^31 through the scalar offset, which every resource rejects:
-    // it reads zeros without touching memory, and every sub-step issues the same loads.
+    // The loads of the group's sub-step t (block sub-step p + 4 t) into buffer t % 4, the sub-step's
+    // offset in the scalar offset. A sub-step past the group's last (t >= nt) adds 2^31 there, which
+    // every resource rejects: it reads zeros without touching memory.
     auto load = [&](WideW& r, int t) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
         uint8_t* const dst = xgrp + (t & 3) * kWideXBuf;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds_dma16(xr, dst + 1024 * (4 * h + q), xo[q] + 128u * u, oob);
+        for (int q = 0; q < 4; ++q) lds_dma16(xr, dst + 1024 * (4 * h + q), xo[q], oob + 128u * u);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo + 512u * u, oob + (uint32_t)j * wfrag, 0);
-        r.s = __builtin_amdgcn_raw_buffer_load_b64(sr, so + 256u * u, oob, 0);
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo, oob + 512u * u + (uint32_t)j * wfrag, 0);
+        r.s = __builtin_amdgcn_raw_buffer_load_b64(sr, so, oob + 256u * u, 0);
     };
 
     const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
@@ -906,61 +929,95 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const WideW& r, const uint8_t* __restrict__ src) {
-        h2 ss[FN];
+    // Weights of MFMA kk of a sub-step: (q - zero) * scale in fp16, exact in the subtraction.
+    auto dequant = [&](const WideW& r, int kk, h8 (&bw)[FN]) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const _Float16 sc = bits_h((uint16_t)(r.s[j >> 1] >> (16 * (j & 1))));
-            ss[j] = (h2){sc, sc};
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            h8 ax[FM], bw[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) ax[i] = *reinterpret_cast<const h8*>(src + 2048 * i + (kk ? rd1 : rd0));
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const uint32_t d = r.w[j][kk], d8 = d >> 8;
-                const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
-                const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
-                const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
-                const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
-                const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss[j]), h2_bits((q1 - zz_hi) * ss[j]),
-                                           h2_bits((q2 - zz_lo) * ss[j]), h2_bits((q3 - zz_hi) * ss[j]));
-                bw[j] = *reinterpret_cast<const h8*>(&u);
-            }
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw[j], acc[i][j], 0, 0, 0);
+            const h2 ss = {sc, sc};
+            const uint32_t d = r.w[j][kk], d8 = d >> 8;
+            const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
+            const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
+            const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
+            const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
+            const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss), h2_bits((q1 - zz_hi) * ss),
+                                       h2_bits((q2 - zz_lo) * ss), h2_bits((q3 - zz_hi) * ss));
+            bw[j] = *reinterpret_cast<const h8*>(&u);
         }
     };
+    auto read_x = [&](int t, h8 (&x0)[FM], h8 (&x1)[FM]) {
+        const uint8_t* src = xgrp + (t & 3) * kWideXBuf;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) x0[i] = *reinterpret_cast<const h8*>(src + 2048 * i + rd0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) x1[i] = *reinterpret_cast<const h8*>(src + 2048 * i + rd1);
+    };
+    auto mfmas = [&](const h8 (&x)[FM], const h8 (&b)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
+    };
 
-    // Sub-step t: wait for this wave's loads of t (those of t + 1 and t + 2 stay in flight), the
-    // barrier, the loads of t + 3 into the buffer t - 1 used, the math. Register sets rotate by four.
     WideW r0, r1, r2, r3;
+    h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
     load(r0, 0);
     load(r1, 1);
     load(r2, 2);
-    auto step = [&](int t, const WideW& cur, WideW& nxt3) {
+    load(r3, 3);
+    wait_vmcnt<3 * kWideLoads>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    read_x(0, ax0, ax1);
+    dequant(r0, 0, bw0);
+
+    // Sub-step t with register set cur (t's operands, refilled with t + 4's) and nx1 (t + 1's). At
+    // the mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
+    auto step = [&](int t, WideW& cur, const WideW& nx1, auto kind) {
+        constexpr bool kLoad = decltype(kind)::load;
+        constexpr int kWait = decltype(kind)::wait;
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<2 * kWideLoads>();
+        mfmas(ax0, bw0);
+        dequant(cur, 1, bw1);
+#pragma unroll
+        for (int m = 0; m < FM * FN; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x0002, 4, 0);  // up to four VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<kWait>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        load(nxt3, t + 3);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(cur, xgrp + (t & 3) * kWideXBuf);
+        h8 x1c[FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) x1c[i] = ax1[i];
+        mfmas(x1c, bw1);
+        read_x(t + 1, ax0, ax1);
+        if constexpr (kLoad) load(cur, t + 4);
+        dequant(nx1, 0, bw0);
+#pragma unroll
+        for (int m = 0; m < FM * FN; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);      // one MFMA
+            if (m < 2 * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // a fragment read
+            if (m < kWideLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
+            __builtin_amdgcn_sched_group_barrier(0x0002, 4, 0);      // up to four VALU
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
+    using Full = WideStep<true, 2 * kWideLoads>;
     // Four sub-steps per iteration and no early exit (an exit between them made the register
-    // allocator keep extra copies of the accumulators and spill).
-    for (int t = 0; t < nt_all; t += 4) {
-        step(t, r0, r3);
-        step(t + 1, r1, r0);
-        step(t + 2, r2, r1);
-        step(t + 3, r3, r2);
+    // allocator keep extra copies of the accumulators and spill); the last four issue no loads.
+    int t = 0;
+    for (; t < nt_all - 4; t += 4) {
+        step(t, r0, r1, Full{});
+        step(t + 1, r1, r2, Full{});
+        step(t + 2, r2, r3, Full{});
+        step(t + 3, r3, r0, Full{});
     }
+    step(t, r0, r1, WideStep<false, 2 * kWideLoads>{});
+    step(t + 1, r1, r2, WideStep<false, kWideLoads>{});
+    step(t + 2, r2, r3, WideStep<false, 0>{});
+    step(t + 3, r3, r0, WideStep<false, 0>{});
 
     // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
     // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
