@@ -821,10 +821,10 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   t + 1, the dequantization of t + 1's kk = 0 weights and the loads of t + 4 into buffer t % 4
 //   and the register set t just finished with. The dequantization VALU work thus runs between
 //   MFMAs of the same wave (interleaved by scheduling groups), and loads have three and a half
-//   sub-steps to land. Every group runs the same number of sub-steps, a multiple of four (the
-//   barrier needs the same count in every wave, and the loop body holds one sub-step per register
-//   set); a sub-step past the group's last reads zeros through an out-of-range offset and adds
-//   nothing. The last four sub-steps issue no loads (their waits count down instead).
+//   sub-steps to land. Every group runs the same number of sub-steps (the barrier needs the same
+//   count in every wave), the largest group's; a sub-step past a group's last reads zeros through
+//   an out-of-range offset and adds nothing. The last one to four sub-steps issue no loads (their
+//   waits count down instead).
 //   Tile order: with the tile count a multiple of 8, the workgroups that share an XCD (every 8th
 //   workgroup id) take a contiguous run of tiles in groups of 4 row tiles, so each XCD's L2 holds
 //   the activations of 4 row tiles and the weights of the column tiles it needs, rather than
@@ -832,15 +832,21 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   Output: the groups' partial tiles go to LDS in output layout (rows of 132 floats, so the
 //   accumulator writes hit 64 distinct banks), and each thread adds 8 neighbouring outputs in
 //   group order (0 + 1 + 2 + 3) and writes them with 16-byte stores.
-constexpr int kWideBM = 64, kWideBN = 128;
-constexpr int kWideSub = 64;                               // K values per sub-step
-constexpr int kWideXBuf = kWideBM * kWideSub * 2;          // one activation buffer (8 KB)
-constexpr int kWideDepth = 4;                              // activation buffers per group
-constexpr int kWideLoads = 4 + 4 + 1;                      // loads per wave and sub-step
-constexpr int kWidePitch = out_pitch(kWideBN / 16);        // floats per row of a staged partial tile
-constexpr int kWideLdsX = 4 * kWideDepth * kWideXBuf;      // 4 groups x 4 buffers
-constexpr int kWideLdsRed = 4 * kWideBM * kWidePitch * 4;  // 4 partial tiles
-constexpr int kWideLds = kWideLdsX > kWideLdsRed ? kWideLdsX : kWideLdsRed;
+constexpr int kWideBN = 128;
+constexpr int kWideSub = 64;                         // K values per sub-step
+constexpr int kWideDepth = 4;                        // activation buffers per group
+constexpr int kWidePitch = out_pitch(kWideBN / 16);  // floats per row of a staged partial tile
+
+// Sizes for FM row fragments (BM = 16 FM rows: 64 for prefill, 32 or 16 for small M).
+template <int FM>
+struct WideShape {
+    static constexpr int kBM = 16 * FM;
+    static constexpr int kXBuf = kBM * kWideSub * 2;          // one activation buffer
+    static constexpr int kLoads = FM + 4 + 1;                 // loads per wave and sub-step
+    static constexpr int kLdsX = 4 * kWideDepth * kXBuf;      // 4 groups x 4 buffers
+    static constexpr int kLdsRed = 4 * kBM * kWidePitch * 4;  // 4 partial tiles
+    static constexpr int kLds = kLdsX > kLdsRed ? kLdsX : kLdsRed;
+};
 
 // One wave's prefill-copy operands of one sub-step: per fragment 16 nibbles (two words), and the
 // four fragments' fp16 scales.
@@ -849,18 +855,22 @@ struct WideW {
     v2u s;
 };
 
-// A sub-step's kind: whether it issues loads, and how many of this wave's loads may stay in flight
-// at its mid-step wait.
-template <bool L, int W>
+// A sub-step's kind: whether it issues loads, how many of this wave's loads may stay in flight at
+// its mid-step wait, and whether it may lie past the last sub-step (then it only waits and syncs).
+template <bool L, int W, bool G = false>
 struct WideStep {
     static constexpr bool load = L;
     static constexpr int wait = W;
+    static constexpr bool guard = G;
 };
 
-template <int YT>
+template <int FM, int YT>
 __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
-    constexpr int FM = 4, FN = 4;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kWideLds];
+    static_assert(FM == 1 || FM == 2 || FM == 4, "q4_gemm_wide: 16, 32 or 64 rows");
+    constexpr int FN = 4;
+    using S = WideShape<FM>;
+    constexpr int BM = S::kBM, kXBuf = S::kXBuf, kLoads = S::kLoads;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
 
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = wid & 3, h = wid >> 2;
@@ -873,12 +883,12 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         by = 4 * grp + r % rows;
         bx = r / rows;
     }
-    const int n0 = bx * kWideBN, m0 = by * kWideBM;
+    const int n0 = bx * kWideBN, m0 = by * BM;
     const int K = a.K;
     const uint32_t nsub_all = (uint32_t)K / kWideSub;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
     const int nsub = a.part ? min(a.split_steps, (int)nsub_all - s_first) : (int)nsub_all;  // the block's
-    const int nt_all = ((nsub + 3) / 4 + 3) & ~3;          // sub-steps every group runs (a multiple of 4)
+    const int nt_all = (nsub + 3) / 4;                     // sub-steps every group runs
     const int nt = nsub > p ? (nsub - p + 3) / 4 : 0;     // the group's own sub-steps
 
     // Rows past M and columns past N read zeros through the range checks (the launcher keeps the
@@ -886,17 +896,18 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
     const rsrc_t wr = make_rsrc(a.wpf, (uint32_t)(((size_t)a.N + 15) / 16 * nsub_all * 512));
     const rsrc_t sr = make_rsrc(a.spf, (uint32_t)(((size_t)a.N + 63) / 64 * nsub_all * 256));
-    // Direct load q (0..3) of wave h: rows 32 h + 8 q + lane / 8 of the tile, LDS slot lane % 8.
-    uint32_t xo[4];
+    // Direct load q (0 .. FM - 1) of wave h: rows 8 FM h + 8 q + lane / 8 of the tile, LDS slot
+    // lane % 8.
+    uint32_t xo[FM];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 32 * h + 8 * q + (lane >> 3), chunk = (lane & 7) ^ ((r >> 1) & 7);
+    for (int q = 0; q < FM; ++q) {
+        const int r = 8 * FM * h + 8 * q + (lane >> 3), chunk = (lane & 7) ^ ((r >> 1) & 7);
         xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
     const uint32_t wfrag = nsub_all * 512u;  // per fragment
     const uint32_t wo = (uint32_t)(n0 + 64 * h) / 16u * wfrag + 8u * lane;
     const uint32_t so = (uint32_t)(n0 + 64 * h) / 64u * nsub_all * 256u + 8u * (16u * (uint32_t)(g >> 1) + c);
-    uint8_t* const xgrp = lds + p * kWideDepth * kWideXBuf;  // the group's buffers
+    uint8_t* const xgrp = lds + p * kWideDepth * kXBuf;  // the group's buffers
     // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot (2 g + kk) ^ (c / 2)
     // ((16 i + c) / 2 % 8 is c / 2): one lane offset per kk, the fragment a constant 2048 i.
     const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
@@ -908,9 +919,9 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
-        uint8_t* const dst = xgrp + (t & 3) * kWideXBuf;
+        uint8_t* const dst = xgrp + (t & 3) * kXBuf;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds_dma16(xr, dst + 1024 * (4 * h + q), xo[q], oob + 128u * u);
+        for (int q = 0; q < FM; ++q) lds_dma16(xr, dst + 1024 * (FM * h + q), xo[q], oob + 128u * u);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
             r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo, oob + 512u * u + (uint32_t)j * wfrag, 0);
@@ -946,7 +957,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         }
     };
     auto read_x = [&](int t, h8 (&x0)[FM], h8 (&x1)[FM]) {
-        const uint8_t* src = xgrp + (t & 3) * kWideXBuf;
+        const uint8_t* src = xgrp + (t & 3) * kXBuf;
 #pragma unroll
         for (int i = 0; i < FM; ++i) x0[i] = *reinterpret_cast<const h8*>(src + 2048 * i + rd0);
 #pragma unroll
@@ -966,78 +977,87 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     load(r1, 1);
     load(r2, 2);
     load(r3, 3);
-    wait_vmcnt<3 * kWideLoads>();
+    wait_vmcnt<3 * kLoads>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read_x(0, ax0, ax1);
     dequant(r0, 0, bw0);
 
     // Sub-step t with register set cur (t's operands, refilled with t + 4's) and nx1 (t + 1's). At
     // the mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
+    constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
     auto step = [&](int t, WideW& cur, const WideW& nx1, auto kind) {
         constexpr bool kLoad = decltype(kind)::load;
         constexpr int kWait = decltype(kind)::wait;
+        const bool live = !decltype(kind)::guard || t < nt_all;
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(ax0, bw0);
-        dequant(cur, 1, bw1);
+        if (live) {
+            mfmas(ax0, bw0);
+            dequant(cur, 1, bw1);
 #pragma unroll
-        for (int m = 0; m < FM * FN; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x0002, 4, 0);  // up to four VALU
+            for (int m = 0; m < FM * FN; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);             // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);  // its share of the VALU
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<kWait>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        h8 x1c[FM];
+        if (live) {
+            h8 x1c[FM];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) x1c[i] = ax1[i];
-        mfmas(x1c, bw1);
-        read_x(t + 1, ax0, ax1);
-        if constexpr (kLoad) load(cur, t + 4);
-        dequant(nx1, 0, bw0);
+            for (int i = 0; i < FM; ++i) x1c[i] = ax1[i];
+            mfmas(x1c, bw1);
+            read_x(t + 1, ax0, ax1);
+            if constexpr (kLoad) load(cur, t + 4);
+            dequant(nx1, 0, bw0);
 #pragma unroll
-        for (int m = 0; m < FM * FN; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);      // one MFMA
-            if (m < 2 * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // a fragment read
-            if (m < kWideLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
-            __builtin_amdgcn_sched_group_barrier(0x0002, 4, 0);      // up to four VALU
+            for (int m = 0; m < FM * FN; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
+                if (m < 2 * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // a fragment read
+                if (m < kLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);        // its share of the VALU
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    using Full = WideStep<true, 2 * kWideLoads>;
-    // Four sub-steps per iteration and no early exit (an exit between them made the register
-    // allocator keep extra copies of the accumulators and spill); the last four issue no loads.
+    using Full = WideStep<true, 2 * kLoads>;
+    // Four sub-steps per iteration and no exit between them (an exit there made the register
+    // allocator keep extra copies of the accumulators and spill). The last four issue no loads (the
+    // loads of the sub-steps up to 3 past them are in flight; those past nt_all read zeros) and their
+    // waits count down; the ones past nt_all only wait and sync.
     int t = 0;
-    for (; t < nt_all - 4; t += 4) {
+    for (; t + 4 < nt_all; t += 4) {
         step(t, r0, r1, Full{});
         step(t + 1, r1, r2, Full{});
         step(t + 2, r2, r3, Full{});
         step(t + 3, r3, r0, Full{});
     }
-    step(t, r0, r1, WideStep<false, 2 * kWideLoads>{});
-    step(t + 1, r1, r2, WideStep<false, kWideLoads>{});
-    step(t + 2, r2, r3, WideStep<false, 0>{});
-    step(t + 3, r3, r0, WideStep<false, 0>{});
+    step(t, r0, r1, WideStep<false, 2 * kLoads>{});
+    step(t + 1, r1, r2, WideStep<false, kLoads, true>{});
+    step(t + 2, r2, r3, WideStep<false, 0, true>{});
+    step(t + 3, r3, r0, WideStep<false, 0, true>{});
 
     // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
     // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
     // group order -> y or the split-K partials.
     wait_vmcnt<0>();
     __syncthreads();
-    float* red = reinterpret_cast<float*>(lds);  // [4 groups][64 rows][kWidePitch]
+    float* red = reinterpret_cast<float*>(lds);  // [4 groups][BM rows][kWidePitch]
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                red[(p * kWideBM + 16 * i + 4 * g + r) * kWidePitch + 64 * h + 16 * j + c] = acc[i][j][r];
+                red[(p * BM + 16 * i + 4 * g + r) * kWidePitch + 64 * h + 16 * j + c] = acc[i][j][r];
     __syncthreads();
     float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
     const bool vec = out8_vector_ok<YT>(a, part);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < (BM * 16 + 511) / 512; ++k) {
         const int u = (int)threadIdx.x + 512 * k;  // chunk of 8 outputs: row u / 16, columns 8 (u % 16)
+        if (BM * 16 < 512 && u >= BM * 16) break;
         const int row = u >> 4, col = (u & 15) * 8;
         const int m = m0 + row, n = n0 + col;
         float v[8];
@@ -1045,9 +1065,9 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e += 4) {
             const float4 s0 = *reinterpret_cast<const float4*>(src + e);
-            const float4 s1 = *reinterpret_cast<const float4*>(src + kWideBM * kWidePitch + e);
-            const float4 s2 = *reinterpret_cast<const float4*>(src + 2 * kWideBM * kWidePitch + e);
-            const float4 s3 = *reinterpret_cast<const float4*>(src + 3 * kWideBM * kWidePitch + e);
+            const float4 s1 = *reinterpret_cast<const float4*>(src + BM * kWidePitch + e);
+            const float4 s2 = *reinterpret_cast<const float4*>(src + 2 * BM * kWidePitch + e);
+            const float4 s3 = *reinterpret_cast<const float4*>(src + 3 * BM * kWidePitch + e);
             v[e] = s0.x + s1.x + s2.x + s3.x;
             v[e + 1] = s0.y + s1.y + s2.y + s3.y;
             v[e + 2] = s0.z + s1.z + s2.z + s3.z;
@@ -1286,14 +1306,26 @@ void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
     BYHIP_LAUNCHED("q4_gemm_skinny");
 }
 
-void launch_q4_wide(const GemmArgs& a, int splits) {
-    const dim3 grid((a.N + kWideBN - 1) / kWideBN, (a.M + kWideBM - 1) / kWideBM, splits);
+template <int FM>
+void launch_q4_wide_shape(const GemmArgs& a, int splits) {
+    const dim3 grid((a.N + kWideBN - 1) / kWideBN, (a.M + 16 * FM - 1) / (16 * FM), splits);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL(q4_gemm_wide<BYHIP_F32>, grid, dim3(512), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL(q4_gemm_wide<BYHIP_F16>, grid, dim3(512), 0, stream(), a); break;
-    default: hipLaunchKernelGGL(q4_gemm_wide<BYHIP_BF16>, grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F32>), grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F16>), grid, dim3(512), 0, stream(), a); break;
+    default: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_BF16>), grid, dim3(512), 0, stream(), a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_wide");
+}
+
+// Rows per tile: 16 or 32 when M fits, else 64.
+int wide_rows(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : 64; }
+
+void launch_q4_wide(const GemmArgs& a, int splits) {
+    switch (wide_rows(a.M)) {
+    case 16: launch_q4_wide_shape<1>(a, splits); break;
+    case 32: launch_q4_wide_shape<2>(a, splits); break;
+    default: launch_q4_wide_shape<4>(a, splits); break;
+    }
 }
 
 template <int BM, int BN>
@@ -1365,12 +1397,12 @@ bool q4_skinny_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 64) * a.gpr * 2 < kLim;
 }
 
-// Whether the wide tile (64 x 128) takes the call: the weights' prefill copy, the pipelined
-// kernel's conditions, K % 128 == 0 and all operand offsets, including the rows and columns a tile
-// reaches past M and N, below 2^31.
+// Whether the wide tile takes the call: the weights' prefill copy (K % 64 == 0), the pipelined
+// kernel's conditions and all operand offsets, including the rows and columns a tile reaches past
+// M and N, below 2^31.
 bool q4_wide_ok(const GemmArgs& a) {
     constexpr uint64_t kLim = 0x80000000u;
-    return a.wpf && a.spf && a.K % 128 == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + 64) * a.K * 2 < kLim &&
+    return a.wpf && a.spf && a.K % kWideSub == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + 64) * a.K * 2 < kLim &&
            (uint64_t)(a.N + 128) * a.row_bytes < kLim && (uint64_t)(a.N + 128) * a.gpr * 2 < kLim;
 }
 
@@ -1400,24 +1432,64 @@ void launch_q4_big(const GemmArgs& a0, int split_choice = 0) {
     if (a.part) launch_splitk_sum(a, splits);
 }
 
+// K splits for the wide tile: the count that minimises the estimated time
+// ceil(tiles * s / CUs) x (sub-steps per split + 16), the 16 standing for a block's fixed cost (its
+// first loads' latency, the epilogue), with at least 8 sub-steps per split and each split a multiple
+// of 4 sub-steps (one per group and round); fewer splits win unless more save over 3 %.
+int wide_splits(const GemmArgs& a, long tiles) {
+    const int nsub = a.K / kWideSub;
+    const long cus = compute_units();
+    int best = 1;
+    double best_t = 1e300;
+    for (int s = 1; s <= std::max(1, nsub / 8); ++s) {
+        const int steps = ((nsub + s - 1) / s + 3) / 4 * 4;
+        const int splits = (nsub + steps - 1) / steps;
+        if (splits != s) continue;  // the same split as a smaller s
+        const double t = (double)((tiles * s + cus - 1) / cus) * (steps + 16);
+        if (t < 0.97 * best_t) {
+            best = s;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
 // Rows per block: 16 or 32 (the smallest that holds M) with 64 columns and two blocks per CU, or
-// the wide 64 x 128 tile (q4_gemm_wide, eight waves) with one block per CU.
+// the wide tile (q4_gemm_wide: 128 columns, 16, 32 or 64 rows, eight waves) with one block per CU.
 void launch_q4_skinny(const GemmArgs& a0, int split_choice = 0, bool wide = false) {
     GemmArgs a = a0;
-    const int bm = wide ? 64 : a.M <= 16 ? 16 : 32, cols = wide ? 128 : 64;
+    const int bm = wide ? wide_rows(a.M) : a.M <= 16 ? 16 : 32, cols = wide ? 128 : 64;
     const long tiles = (long)((a.N + cols - 1) / cols) * ((a.M + bm - 1) / bm);
     // the wide kernel counts 64-value sub-steps, the skinny one 128-value steps
-    int splits = wide ? choose_split(a, tiles, a.K / kWideSub, 16, split_choice, 1)
-                      : choose_split(a, tiles, a.K / 128, 8, split_choice, 2);
-    if (wide && a.part) {
-        // slices of whole rounds of the wide kernel's loop: 4 groups x 4 sub-steps
-        a.split_steps = (a.split_steps + 15) / 16 * 16;
-        splits = (a.K / kWideSub + a.split_steps - 1) / a.split_steps;
+    int splits;
+    if (wide) {
+        const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
+        splits = choose_split(a, tiles, a.K / kWideSub, 1, forced > 0 ? forced : wide_splits(a, tiles), 1);
+        if (a.part) {
+            // whole rounds of the four groups
+            a.split_steps = (a.split_steps + 3) / 4 * 4;
+            splits = (a.K / kWideSub + a.split_steps - 1) / a.split_steps;
+        }
+        if (splits == 1) a.part = nullptr;
+    } else {
+        splits = choose_split(a, tiles, a.K / 128, 8, split_choice, 2);
     }
     if (wide) launch_q4_wide(a, splits);
     else if (bm == 16) launch_q4_skinny_shape<16, 4>(a, splits);
     else launch_q4_skinny_shape<32, 4>(a, splits);
     if (a.part) launch_splitk_sum(a, splits);
+}
+
+// Whether a small-M call (the skinny kernel's range) takes the wide tile: when the weights have the
+// prefill copy and the wide grid keeps at least 16 sub-steps per K split. Measured on MI355X (M = 9
+// to 32, weights streamed from HBM): the wide tile is 8-30 % faster on K x N = 4096 x 6144,
+// 4096 x 28672 and 14336 x 4096, and 15-25 % slower on 4096 x 4096, whose 32 column tiles need 8
+// splits of 8 sub-steps.
+bool q4_small_wide(const GemmArgs& a) {
+    if (!q4_wide_ok(a)) return false;
+    const long tiles = (long)((a.N + kWideBN - 1) / kWideBN) * ((a.M + wide_rows(a.M) - 1) / wide_rows(a.M));
+    const int splits = wide_splits(a, tiles), nsub = a.K / kWideSub;
+    return (nsub + splits - 1) / splits >= 16;
 }
 
 // Splits launch_q4_big chooses: K is split when the tiles fill at most half the CUs, into as many
@@ -1540,7 +1612,7 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     switch (fmt) {
     case BFormat::Q4Fast:
         if (q4_skinny_ok(a)) {
-            launch_q4_skinny(a);
+            launch_q4_skinny(a, 0, q4_small_wide(a));
             break;
         }
         switch (q4_prefill_kind(a)) {

@@ -14,7 +14,7 @@ enum Q4PlanKind : int {
     kPlanSkinny = 4,   // the skinny MFMA GEMM (M <= 32)
     kPlanGemm = 5,     // the general LDS-staged MFMA GEMM
     kPlanBig = 6,      // the 128 x 256 prefill tile
-    kPlanWide = 7,     // the 64 x 128 skinny prefill tile
+    kPlanWide = 7,     // the wide tile (128 columns; 16, 32 or 64 rows)
     kPlanExact = 8,    // the exact fp32 MFMA GEMM
     kPlanLast = kPlanExact
 };

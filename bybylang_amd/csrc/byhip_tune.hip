@@ -167,6 +167,26 @@ bool tuning_enabled() {
 }
 
 constexpr size_t kScrubBytes = (size_t)512 << 20;
+constexpr int kScrubBlocks = 1024;
+
+// Reads every 16-byte word of `buf` (n words), so that the caches and address translations hold
+// other, clean data, as after other weights streamed through; each block's XOR of what it read
+// goes to sink[block] (the reads are then not dead code).
+__global__ __launch_bounds__(256) void scrub_read(const uint4* __restrict__ buf, size_t n, uint32_t* sink) {
+    uint32_t v = 0;
+    for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (size_t)kScrubBlocks * 256) {
+        const uint4 q = buf[i];
+        v ^= q.x ^ q.y ^ q.z ^ q.w;
+    }
+    __shared__ uint32_t red[256];
+    red[threadIdx.x] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t r = 0;
+        for (int i = 0; i < 256; ++i) r ^= red[i];
+        sink[blockIdx.x] = r;
+    }
+}
 
 struct Candidate {
     Q4Plan plan;
@@ -182,8 +202,10 @@ std::vector<Candidate> candidates(int mt, int x_dtype) {
     if (x_dtype == BYHIP_F16) {
         for (int tile = 1; tile <= 4; ++tile)
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanPipe, tile, sp}, 3e-3f});
-        if (mt <= 32)
+        if (mt <= 32) {
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanSkinny, 0, sp}, 3e-3f});
+            for (int sp : {0, 1, 2, 4, 8}) c.push_back({{kPlanWide, 0, sp}, 3e-3f});
+        }
         if (mt > 32) {
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanBig, 0, sp}, 3e-3f});
             for (int sp : {0, 1, 2}) c.push_back({{kPlanWide, 0, sp}, 3e-3f});
@@ -213,8 +235,8 @@ PlanEntry tune(const byhip_q4w* w, int M, int x_dtype) {
     }
     void* dx = device_alloc(nx * xb);
     float* dy = static_cast<float*>(device_alloc(ny * 4));
-    void* scrub = nullptr;
-    if (hipMalloc(&scrub, kScrubBytes) != hipSuccess) {  // without it the timing runs warm
+    void* scrub = nullptr;  // kScrubBytes to read, then the blocks' sink words
+    if (hipMalloc(&scrub, kScrubBytes + kScrubBlocks * sizeof(uint32_t)) != hipSuccess) {  // else warm timing
         (void)hipGetLastError();
         scrub = nullptr;
     }
@@ -225,6 +247,7 @@ PlanEntry tune(const byhip_q4w* w, int M, int x_dtype) {
                                  nx * xb, hipMemcpyHostToDevice, stream()));
         BYHIP_HIP(hipEventCreate(&e0));
         BYHIP_HIP(hipEventCreate(&e1));
+        if (scrub) BYHIP_HIP(hipMemsetAsync(scrub, 0x5A, kScrubBytes, stream()));
         auto run_once = [&](const Q4Plan& p, std::vector<float>& out) {
             if (!q4_run_plan(p, dx, x_dtype, w, dy, BYHIP_F32, mt)) return false;
             out.resize(ny);
@@ -232,13 +255,20 @@ PlanEntry tune(const byhip_q4w* w, int M, int x_dtype) {
             BYHIP_HIP(hipStreamSynchronize(stream()));
             return true;
         };
-        // Each timed run starts cold: a scrub buffer twice the Infinity Cache is rewritten first
-        // (outside the events), so the weights come from HBM as they do when a model's layers
-        // stream through; repeated runs on the same weights would otherwise time cache hits.
+        // Each timed run starts cold: a scrub buffer twice the Infinity Cache is read first (outside
+        // the events), so the weights come from HBM as they do when a model's layers stream
+        // through, and the caches hold clean lines as they do then (a rewrite would leave dirty
+        // lines whose write-back slows the timed kernel); repeated runs on the same weights would
+        // otherwise time cache hits.
         auto time_ms = [&](const Q4Plan& p, int reps) {
             float total = 0.0f;
             for (int r = 0; r < reps; ++r) {
-                if (scrub) BYHIP_HIP(hipMemsetAsync(scrub, r & 0xFF, kScrubBytes, stream()));
+                if (scrub) {
+                    hipLaunchKernelGGL(scrub_read, dim3(kScrubBlocks), dim3(256), 0, stream(),
+                                       static_cast<const uint4*>(scrub), kScrubBytes / 16,
+                                       reinterpret_cast<uint32_t*>(static_cast<char*>(scrub) + kScrubBytes));
+                    BYHIP_LAUNCHED("scrub_read");
+                }
                 BYHIP_HIP(hipEventRecord(e0, stream()));
                 q4_run_plan(p, dx, x_dtype, w, dy, BYHIP_F32, mt);
                 BYHIP_HIP(hipEventRecord(e1, stream()));
@@ -279,6 +309,9 @@ PlanEntry tune(const byhip_q4w* w, int M, int x_dtype) {
             }
         size_t best = 0;
         for (auto& s : samples) std::sort(s.begin(), s.end());
+        if (getenv("BYHIP_Q4_TUNE_VERBOSE"))
+            for (size_t i = 0; i < valid.size(); ++i)
+                fprintf(stderr, "[q4-tune:hip]   %s %.4f ms\n", plan_name(valid[i]).c_str(), samples[i][1]);
         for (size_t i = 1; i < valid.size(); ++i)
             if (samples[i][1] < samples[best][1] * 0.97f) best = i;
         best_entry.plan = valid[best];

@@ -229,6 +229,32 @@ def test_q4_gemm_prefill_tiles(hip, oracle, monkeypatch, kind, shape, splits, gr
     tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
 
 
+@pytest.mark.parametrize("M", [1, 5, 9, 16, 17, 31, 32])
+@pytest.mark.parametrize("splits", [0, 3, 5])
+@pytest.mark.parametrize("group", [32, 0])
+def test_q4_gemm_wide_small_m(hip, oracle, monkeypatch, M, splits, group):
+    """The wide tile with 16 and 32 rows (forced for small M): ragged M, K and N, K split so that
+    the groups' sub-step counts differ and the last sub-steps lie past the end (K = 1344: 21
+    sub-steps of 64), fp16 in and out, against the oracle; a repeat call is bit-identical."""
+    from bybylang_amd import synth
+    K, N = 1344, 264
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_SKINNY_MAX_M", "0")
+    monkeypatch.setenv("BYHIP_Q4_PREFILL", "3")
+    if splits:
+        monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
+    g = synth.rng(7700 + 13 * M + group + splits)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K, group if group else K)
+    gpr = K // group if group else 1
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 wide small M={M} splits={splits} group={group}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    again, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    assert np.array_equal(got, again)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, group, gpr)
+    tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
 @pytest.mark.parametrize("kind", ["big", "wide"])
 @pytest.mark.parametrize("y_dtype", ["F32", "BF16"])
 def test_q4_gemm_prefill_out_dtypes(hip, oracle, monkeypatch, kind, y_dtype):
