@@ -815,12 +815,14 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   at slot c ^ ((r / 2) % 8): the fragment reads (16 rows, one chunk each) then hit 16 distinct
 //   bank groups. Four buffers per group.
 //   Sub-step t of a group runs in two halves around one block barrier: the kk = 0 MFMAs beside
-//   the dequantization of the kk = 1 weights; the wait for this wave's loads of t + 1 and the
-//   barrier (which publishes every wave's direct loads of t + 1 and, since each wave's fragment
-//   reads of t have returned, frees buffer t % 4); the kk = 1 MFMAs beside the fragment reads of
-//   t + 1, the dequantization of t + 1's kk = 0 weights and the loads of t + 4 into buffer t % 4
-//   and the register set t just finished with. The dequantization VALU work thus runs between
-//   MFMAs of the same wave (interleaved by scheduling groups), and loads have three and a half
+//   the dequantization of the kk = 1 weights and the weight loads of t + 3 (into the register set
+//   t - 1 finished with); the wait for this wave's loads of t + 1 and the barrier (which publishes
+//   every wave's direct loads of t + 1 and, since each wave's fragment reads of t have returned,
+//   frees buffer t % 4); the kk = 1 MFMAs beside the fragment reads of t + 1, the dequantization
+//   of t + 1's kk = 0 weights and the activation loads of t + 4 into buffer t % 4. The
+//   dequantization VALU work thus runs between MFMAs of the same wave (interleaved by scheduling
+//   groups), the loads are spread over both halves (8 % faster at K = 14336 than all in the
+//   second), and loads have two and a half to three and a half
 //   sub-steps to land. Every group runs the same number of sub-steps (the barrier needs the same
 //   count in every wave), the largest group's; a sub-step past a group's last reads zeros through
 //   an out-of-range offset and adds nothing. The last one to four sub-steps issue no loads (their
@@ -855,11 +857,13 @@ struct WideW {
     v2u s;
 };
 
-// A sub-step's kind: whether it issues loads, how many of this wave's loads may stay in flight at
-// its mid-step wait, and whether it may lie past the last sub-step (then it only waits and syncs).
-template <bool L, int W, bool G = false>
+// A sub-step's kind: whether it issues activation loads (of 4 sub-steps ahead) and weight loads
+// (of 3 ahead), how many of this wave's loads may stay in flight at its mid-step wait, and whether
+// it may lie past the last sub-step (then it only waits and syncs).
+template <bool L, bool LW, int W, bool G = false>
 struct WideStep {
     static constexpr bool load = L;
+    static constexpr bool load_ws = LW;
     static constexpr int wait = W;
     static constexpr bool guard = G;
 };
@@ -912,16 +916,22 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // ((16 i + c) / 2 % 8 is c / 2): one lane offset per kk, the fragment a constant 2048 i.
     const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
 
-    // The loads of the group's sub-step t (block sub-step p + 4 t) into buffer t % 4, the sub-step's
-    // offset in the scalar offset. A sub-step past the group's last (t >= nt) adds 2^31 there, which
+    // The loads of the group's sub-step t (block sub-step p + 4 t): its activations into buffer t % 4
+    // (FM direct loads), its weights and scales into a register set (5 loads); the sub-step's offset
+    // goes in the scalar offset. A sub-step past the group's last (t >= nt) adds 2^31 there, which
     // every resource rejects: it reads zeros without touching memory.
-    auto load = [&](WideW& r, int t) {
+    auto load_x = [&](int t) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
         uint8_t* const dst = xgrp + (t & 3) * kXBuf;
 #pragma unroll
         for (int q = 0; q < FM; ++q) lds_dma16(xr, dst + 1024 * (FM * h + q), xo[q], oob + 128u * u);
+    };
+    auto load_ws = [&](WideW& r, int t) {
+        const bool ok = t < nt;
+        const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
+        const uint32_t oob = ok ? 0u : 0x80000000u;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
             r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo, oob + 512u * u + (uint32_t)j * wfrag, 0);
@@ -971,21 +981,28 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
     };
 
+    // Issue order: sub-step t's activations, then its weights (t = 0, 1, 2), and sub-step 3's
+    // activations; sub-step 3's weights follow in sub-step 0.
     WideW r0, r1, r2, r3;
     h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
-    load(r0, 0);
-    load(r1, 1);
-    load(r2, 2);
-    load(r3, 3);
-    wait_vmcnt<3 * kLoads>();
+    load_x(0);
+    load_ws(r0, 0);
+    load_x(1);
+    load_ws(r1, 1);
+    load_x(2);
+    load_ws(r2, 2);
+    load_x(3);
+    wait_vmcnt<2 * kLoads + FM>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read_x(0, ax0, ax1);
     dequant(r0, 0, bw0);
 
-    // Sub-step t with register set cur (t's operands, refilled with t + 4's) and nx1 (t + 1's). At
-    // the mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
+    // Sub-step t with register sets cur (t's operands), nx1 (t + 1's) and nx3 (refilled with t + 3's
+    // weights in the first half, once cur's last fragments are dequantized: the loads stay spread
+    // over both halves). The second half issues t + 4's activations into buffer t % 4. At the
+    // mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
     constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
-    auto step = [&](int t, WideW& cur, const WideW& nx1, auto kind) {
+    auto step = [&](int t, WideW& cur, const WideW& nx1, WideW& nx3, auto kind) {
         constexpr bool kLoad = decltype(kind)::load;
         constexpr int kWait = decltype(kind)::wait;
         const bool live = !decltype(kind)::guard || t < nt_all;
@@ -993,10 +1010,12 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         if (live) {
             mfmas(ax0, bw0);
             dequant(cur, 1, bw1);
+            if constexpr (decltype(kind)::load_ws) load_ws(nx3, t + 3);
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);             // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);  // its share of the VALU
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                          // one MFMA
+                if (m < FN + 1) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);         // a load
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);               // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1009,34 +1028,35 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             for (int i = 0; i < FM; ++i) x1c[i] = ax1[i];
             mfmas(x1c, bw1);
             read_x(t + 1, ax0, ax1);
-            if constexpr (kLoad) load(cur, t + 4);
+            if constexpr (kLoad) load_x(t + 4);
             dequant(nx1, 0, bw0);
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
                 __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
                 if (m < 2 * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // a fragment read
-                if (m < kLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
+                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);       // a load
                 __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);        // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    using Full = WideStep<true, 2 * kLoads>;
+    using Full = WideStep<true, true, 2 * kLoads>;
     // Four sub-steps per iteration and no exit between them (an exit there made the register
-    // allocator keep extra copies of the accumulators and spill). The last four issue no loads (the
-    // loads of the sub-steps up to 3 past them are in flight; those past nt_all read zeros) and their
-    // waits count down; the ones past nt_all only wait and sync.
+    // allocator keep extra copies of the accumulators and spill). Of the last four only the first
+    // issues loads (the weights of the last sub-step); the loads of the sub-steps up to 3 past them
+    // are in flight (those past nt_all read zeros), and their waits count down; the ones past
+    // nt_all only wait and sync.
     int t = 0;
     for (; t + 4 < nt_all; t += 4) {
-        step(t, r0, r1, Full{});
-        step(t + 1, r1, r2, Full{});
-        step(t + 2, r2, r3, Full{});
-        step(t + 3, r3, r0, Full{});
+        step(t, r0, r1, r3, Full{});
+        step(t + 1, r1, r2, r0, Full{});
+        step(t + 2, r2, r3, r1, Full{});
+        step(t + 3, r3, r0, r2, Full{});
     }
-    step(t, r0, r1, WideStep<false, 2 * kLoads>{});
-    step(t + 1, r1, r2, WideStep<false, kLoads, true>{});
-    step(t + 2, r2, r3, WideStep<false, 0, true>{});
-    step(t + 3, r3, r0, WideStep<false, 0, true>{});
+    step(t, r0, r1, r3, WideStep<false, true, 2 * kLoads>{});
+    step(t + 1, r1, r2, r0, WideStep<false, false, kLoads, true>{});
+    step(t + 2, r2, r3, r1, WideStep<false, false, 0, true>{});
+    step(t + 3, r3, r0, r2, WideStep<false, false, 0, true>{});
 
     // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
     // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
