@@ -1097,211 +1097,243 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     }
 }
 
-// Large-tile Q4 GEMM for prefill: a 128 x 256 tile per block, so each activation byte is read once
-// per 256 columns and each weight byte once per 128 rows. Every operand byte reaches the CU as an
-// L1-to-L2 request, and the bytes each CU must pull that way bound the smaller tiles at these
-// shapes; the larger tile needs about half the bytes per output.
-//   Block: 4 waves; wave w owns columns 64w .. 64w+63 of the tile and all 128 rows (8 x 4
-//   fragments, 128 accumulators), and the block shares the activation tile.
-//   K steps of 128: in MFMA kk (0..3) lane group g supplies values 32g + 8kk .. 32g + 8kk + 7 in
-//   natural order; a lane's weights for a step are one 16-byte load of one 32-value group, and its
-//   scale.
-//   Activations: the step's 128 x 128 slice moves straight from global memory into LDS with direct
-//   loads (wave w the rows 32w .. 32w+31, 16 lanes per row), chunk c of row r at slot c ^ (r & 15)
-//   as in the skinny kernel. Three LDS buffers and three weight register sets keep the loads of the
-//   next two steps in flight while a step computes. One barrier per step, after each wave's wait
-//   for its own loads of the step, makes every wave's direct loads visible and tells the block that
-//   the buffer the next loads overwrite (read two steps earlier) is free.
-//   Split-K: block z covers the K steps [z * split_steps, ...) and writes fp32 partials.
-constexpr int kBigM = 128, kBigN = 256;
-constexpr int kBigBuf = kBigM * 256;            // bytes of one activation buffer
-constexpr int kBigFM = kBigM / 16, kBigFN = 4;  // fragments per wave
-constexpr int kBigLoads = kBigM / 16 + 2 * kBigFN;  // vector memory instructions per wave and step
+// Tall Q4 GEMM for large prefill shapes: a 128 x 256 tile per block on the prefill copy, so that
+// each activation byte reaches the CU once per 256 columns and each weight byte once per 128 rows
+// (about half the operand bytes per output of the 64 x 128 wide tile).
+//   Block: eight waves, two per SIMD; wave w owns columns 32 w .. 32 w + 31 (2 fragments) and all
+//   128 rows (8 fragments), 64 accumulators; every wave runs every 64-value sub-step, so each
+//   dequantized fragment feeds 8 MFMAs (about 2 VALU per MFMA) and each activation fragment read
+//   from LDS feeds 2.
+//   Operands as in the wide tile: natural K order from the copy's nibble order; a wave's weights
+//   for a sub-step are two 8-byte loads and its 2 fragments' scales one 4-byte load; the block's
+//   activation slice (128 rows x 128 bytes, 16 KB) moves straight into LDS, each wave loading 16
+//   rows, XOR-swizzled as in the wide tile. Four buffers.
+//   Sub-step t runs in two halves around one block barrier: the kk = 0 MFMAs beside the fragment
+//   reads of t's kk = 1 activations, the dequantization of t's kk = 1 weights and the weight loads
+//   of t + 3; the wait for this wave's loads of t + 1 and the barrier (which publishes every wave's
+//   direct loads of t + 1 and, every wave's reads of t having returned, frees buffer t % 4); the
+//   kk = 1 MFMAs beside the reads of t + 1's kk = 0 activations, the dequantization of t + 1's
+//   kk = 0 weights and the activation loads of t + 4 into buffer t % 4. The last four sub-steps
+//   issue no activation loads, and those past the last only wait and sync.
+//   Output: each wave stages its 128 x 32 block in LDS (rows of 36 floats: the accumulator writes
+//   hit 64 distinct banks) and writes it as 16-byte stores of 8 outputs; no cross-wave sums.
+//   Split-K: block z covers the sub-steps [z * split_steps, ...) and writes fp32 partials.
+constexpr int kTallBM = 128, kTallBN = 256;
+constexpr int kTallXBuf = kTallBM * kWideSub * 2;           // one activation buffer (16 KB)
+constexpr int kTallLoads = 2 + 2 + 1;                       // loads per wave and sub-step
+constexpr int kTallPitch = 32 + 4;                          // floats per row of a wave's staged block
+constexpr int kTallLdsX = 4 * kTallXBuf;
+constexpr int kTallLdsOut = 8 * kTallBM * kTallPitch * 4;  // the eight waves' staged blocks
+constexpr int kTallLds = kTallLdsX > kTallLdsOut ? kTallLdsX : kTallLdsOut;
 
-struct BigW {
-    v4u w[kBigFN];       // 32 nibbles of one column per fragment
-    uint32_t s[kBigFN];  // their fp16 scale
+// One wave's prefill-copy operands of one sub-step: per fragment 16 nibbles (two words), and the
+// two fragments' fp16 scales.
+struct TallW {
+    v2u w[2];
+    uint32_t s;
 };
 
-// Waits for this wave's loads except the newest N, then the workgroup barrier; the memory clobber
-// keeps LDS accesses on their side of it, and the direct loads issued last stay in flight.
-template <int N>
-__device__ __forceinline__ void lds_step_barrier() {
-    wait_vmcnt<N>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 template <int YT>
-__global__ __launch_bounds__(256, 1) void q4_gemm_big(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kBigBuf];
+__global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
+    constexpr int FM = 8, FN = 2;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kTallLds];
 
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * kBigN, m0 = blockIdx.y * kBigM;
+    int bx = blockIdx.x, by = blockIdx.y;
+    {
+        // the wide tile's XCD-grouped tile order
+        const int gx = gridDim.x, gy = gridDim.y, tiles = gx * gy, id = bx + gx * by;
+        const int j = tiles % 8 == 0 ? (id % 8) * (tiles / 8) + id / 8 : id;
+        const int grp = j / (4 * gx), rows = min(4, gy - 4 * grp), r = j % (4 * gx);
+        by = 4 * grp + r % rows;
+        bx = r / rows;
+    }
+    const int n0 = bx * kTallBN, m0 = by * kTallBM, col0 = n0 + 32 * wid;
     const int K = a.K;
+    const uint32_t nsub_all = (uint32_t)K / kWideSub;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
-    const int nsteps = a.part ? min(a.split_steps, K / 128 - s_first) : K / 128;  // the block's steps
+    const int nt = a.part ? min(a.split_steps, (int)nsub_all - s_first) : (int)nsub_all;  // the block's sub-steps
 
-    // Rows past M and columns past N read zeros through the range checks (the launcher keeps every
-    // offset, with the rows and columns the tile reaches past M and N, below 2^31).
+    // Rows past M and columns past N read zeros through the range checks (the launcher keeps the
+    // offsets below 2^31; the prefill copy pads N to whole fragments).
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
-    const rsrc_t wr = make_rsrc(a.wq, (uint32_t)((size_t)a.N * a.row_bytes));
-    // Scales from the blocked copy when there is one (2 lines per fragment load), else row-major.
-    const bool sblk = a.sblk != nullptr;
-    const uint32_t G = (uint32_t)K >> 5;
-    const rsrc_t sr = sblk ? make_rsrc(a.sblk, (uint32_t)(((size_t)a.N + 7) / 8 * 8 * G * 2))
-                           : make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
-    const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
-
-    // Direct load u (0..7) of wave w: lane -> row 32w + 4u + lane / 16, LDS slot lane % 16 holding
-    // chunk slot ^ (row & 15). Loads u and u + 4 share the slot pattern; the rest of each offset is
-    // wave-uniform and goes in the scalar offset, as does each column fragment's row.
-    uint32_t xo[4];
+    const rsrc_t wr = make_rsrc(a.wpf, (uint32_t)(((size_t)a.N + 15) / 16 * nsub_all * 512));
+    const rsrc_t sr = make_rsrc(a.spf, (uint32_t)(((size_t)a.N + 63) / 64 * nsub_all * 256));
+    // Direct load q (0, 1) of wave w: rows 16 w + 8 q + lane / 8 of the tile, LDS slot lane % 8.
+    uint32_t xo[2];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 32 * wid + 4 * q + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+    for (int q = 0; q < 2; ++q) {
+        const int r = 16 * wid + 8 * q + (lane >> 3), chunk = (lane & 7) ^ ((r >> 1) & 7);
         xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
-    const uint32_t xrow16 = 16u * (uint32_t)K * 2u;
-    const int ncol = n0 + 64 * wid + c;
-    const uint32_t wo = (uint32_t)ncol * (uint32_t)a.row_bytes + 16u * g;
-    const uint32_t so = sblk ? 2u * (((uint32_t)ncol >> 3) * G * 8u + 8u * g + (ncol & 7)) : (uint32_t)ncol * (uint32_t)a.gpr;
-    const uint32_t wfrag = 16u * (uint32_t)a.row_bytes, sfrag = sblk ? 32u * G : 32u * (uint32_t)a.gpr;
-    uint8_t* const xdst = lds + 32 * 256 * wid;  // this wave's rows of each buffer
+    const uint32_t wfrag = nsub_all * 512u;  // per fragment
+    const uint32_t wo = (uint32_t)col0 / 16u * wfrag + 8u * lane;
+    // the wave's 2 fragments are fragments 2 (w % 2) and 2 (w % 2) + 1 of their quad
+    const uint32_t so = (uint32_t)col0 / 64u * nsub_all * 256u + 8u * (16u * (uint32_t)(g >> 1) + c) + 4u * (wid & 1);
+    const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
 
-    // A step past the block's last one adds 2^31 through the scalar offset: every resource rejects
-    // it, so it reads zeros without touching memory and every step issues the same loads.
-    auto load = [&](BigW& r, int buf, int t) {
-        const bool ok = t < nsteps;
-        const uint32_t k0 = (uint32_t)(s_first + (ok ? t : 0)) * 128u;
+    // Loads of sub-step t (the sub-step's offset in the scalar offset; past the last, 2^31 there
+    // reads zeros): its activations into buffer t % 4, its weights and scales into a register set.
+    auto load_x = [&](int t) {
+        const bool ok = t < nt;
+        const uint32_t u = (uint32_t)(s_first + (ok ? t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
-        const uint32_t grp = a.group ? ((k0 >> 5) + g) >> gshift : 0u;
-        const uint32_t soff = sblk ? so + 16u * (k0 >> 5) : 2u * (so + grp);
-        uint8_t* const dst = xdst + buf * kBigBuf;
+        uint8_t* const dst = lds + (t & 3) * kTallXBuf;
 #pragma unroll
-        for (int u = 0; u < kBigM / 16; ++u)
-            lds_dma16(xr, dst + 1024 * u, xo[u & 3] + 2u * k0, oob + (uint32_t)(u >> 2) * xrow16);
+        for (int q = 0; q < 2; ++q) lds_dma16(xr, dst + 1024 * (2 * wid + q), xo[q], oob + 128u * u);
+    };
+    auto load_ws = [&](TallW& r, int t) {
+        const bool ok = t < nt;
+        const uint32_t u = (uint32_t)(s_first + (ok ? t : 0));
+        const uint32_t oob = ok ? 0u : 0x80000000u;
 #pragma unroll
-        for (int j = 0; j < kBigFN; ++j)
-            r.w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo + (k0 >> 1), oob + (uint32_t)j * wfrag, 2);
-#pragma unroll
-        for (int j = 0; j < kBigFN; ++j)
-            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, oob + (uint32_t)j * sfrag, 0);
+        for (int j = 0; j < FN; ++j)
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, wo, oob + 512u * u + (uint32_t)j * wfrag, 0);
+        r.s = __builtin_amdgcn_raw_buffer_load_b32(sr, so, oob + 256u * u, 0);
     };
 
-    // Natural-order dequantization: v_perm_b32 copies byte b of the word (values 2b, 2b + 1) to
-    // bytes 0 and 2, the AND-OR keeps the low nibble in the low half and the high nibble in bits
-    // 4-7 of the high half against the exponent word 0x5400 6400: (1024 + q[2b], 64 + q[2b + 1]),
-    // both exact. The activations then need no permutation.
-    const h2 zz = {(_Float16)(1024.0f + a.zero_value), (_Float16)(64.0f + a.zero_value)};
-    uint32_t mag;
-    asm volatile("v_mov_b32 %0, 0x54006400" : "=v"(mag));
+    const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
+    const h2 zz_lo = {zlo, zlo}, zz_hi = {zhi, zhi};
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
 
-    f4 acc[kBigFM][kBigFN];
+    f4 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < kBigFM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < kBigFN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const BigW& r, int buf) {
-        const uint8_t* const src = lds + buf * kBigBuf;
-        h2 ss[kBigFN];
+    // Weights of MFMA kk of a sub-step: (q - zero) * scale in fp16, exact in the subtraction.
+    auto dequant = [&](const TallW& r, int kk, h8 (&bw)[FN]) {
 #pragma unroll
-        for (int j = 0; j < kBigFN; ++j) {
-            const _Float16 sc = bits_h((uint16_t)r.s[j]);
-            ss[j] = (h2){sc, sc};
-        }
-        // the activation fragments of MFMA column kk, read one column ahead of the math
-        uint4 xv[2][kBigFM];
-        auto xread = [&](int kk) {
-#pragma unroll
-            for (int i = 0; i < kBigFM; ++i)
-                xv[kk & 1][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
-        };
-        // Unit u = (kk, j) = (u / 4, u % 4): fragment j's weights of MFMA column kk against the 8
-        // row fragments. The weights of unit u + 1 are dequantized before unit u's MFMAs are
-        // issued, so the compiler can interleave that VALU work with them (explicit scheduling
-        // groups of one MFMA and two VALU instructions measured slower: hazard waits).
-        auto dequant = [&](int u) {
-            const uint32_t d = r.w[u & 3][u >> 2];
-            uint32_t q[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint32_t rep = __builtin_amdgcn_perm(d, d, 0x01010101u * (uint32_t)b);
-                q[b] = h2_bits((bits_h2((rep & 0x00F0000Fu) | mag) - zz) * ss[u & 3]);
-            }
-            const uint4 v = make_uint4(q[0], q[1], q[2], q[3]);
-            return *reinterpret_cast<const h8*>(&v);
-        };
-        xread(0);
-        h8 ax[kBigFM];
-        h8 bw = dequant(0);
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int kk = u >> 2, j = u & 3;
-            if (j == 0) {
-#pragma unroll
-                for (int i = 0; i < kBigFM; ++i) ax[i] = *reinterpret_cast<const h8*>(&xv[kk & 1][i]);
-                if (kk < 3) xread(kk + 1);
-            }
-            const h8 bn = u < 15 ? dequant(u + 1) : bw;
-#pragma unroll
-            for (int i = 0; i < kBigFM; ++i)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i], bw, acc[i][j], 0, 0, 0);
-            bw = bn;
+        for (int j = 0; j < FN; ++j) {
+            const _Float16 sc = bits_h((uint16_t)(r.s >> (16 * j)));
+            const h2 ss = {sc, sc};
+            const uint32_t d = r.w[j][kk], d8 = d >> 8;
+            const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
+            const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
+            const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
+            const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
+            const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss), h2_bits((q1 - zz_hi) * ss),
+                                       h2_bits((q2 - zz_lo) * ss), h2_bits((q3 - zz_hi) * ss));
+            bw[j] = *reinterpret_cast<const h8*>(&u);
         }
     };
+    // The kk half of sub-step t's activation fragments.
+    auto read_x = [&](int t, int kk, h8 (&x)[FM]) {
+        const uint8_t* src = lds + (t & 3) * kTallXBuf + (kk ? rd1 : rd0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) x[i] = *reinterpret_cast<const h8*>(src + 2048 * i);
+    };
+    auto mfmas = [&](const h8 (&x)[FM], const h8 (&b)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
+    };
 
-    // Step t: its loads have landed once only the next step's remain; the barrier; the loads of
-    // step t + 2 into the buffer step t - 1 used; the math.
-    BigW r0, r1, r2;
-    load(r0, 0, 0);
-    load(r1, 1, 1);
-    auto step = [&](int t, const BigW& cur, int cbuf, BigW& nxt2, int nbuf) {
+    // Issue order: sub-step t's activations, then its weights (t = 0, 1, 2), and sub-step 3's
+    // activations; sub-step 3's weights follow in sub-step 0.
+    TallW r0, r1, r2, r3;
+    h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
+    load_x(0);
+    load_ws(r0, 0);
+    load_x(1);
+    load_ws(r1, 1);
+    load_x(2);
+    load_ws(r2, 2);
+    load_x(3);
+    wait_vmcnt<2 * kTallLoads + 2>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    read_x(0, 0, ax0);
+    dequant(r0, 0, bw0);
+
+    constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
+    // Sub-step t with register sets cur (t's operands), nx1 (t + 1's) and nx3 (refilled with t + 3's
+    // weights); at the mid-step wait the loads of t + 2 and t + 3 may stay in flight, those issued.
+    auto step = [&](int t, const TallW& cur, const TallW& nx1, TallW& nx3, auto kind) {
+        constexpr int kWait = decltype(kind)::wait;
+        const bool live = !decltype(kind)::guard || t < nt;
         __builtin_amdgcn_sched_barrier(0);
-        lds_step_barrier<kBigLoads>();
+        if (live) {
+            mfmas(ax0, bw0);
+            read_x(t, 1, ax1);
+            dequant(cur, 1, bw1);
+            if constexpr (decltype(kind)::load_ws) load_ws(nx3, t + 3);
+#pragma unroll
+            for (int m = 0; m < FM * FN; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
+                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);       // a fragment read
+                if (m < FN + 1) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);        // its share of the VALU
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
-        load(nxt2, nbuf, t + 2);
+        wait_vmcnt<kWait>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        compute(cur, cbuf);
+        if (live) {
+            mfmas(ax1, bw1);
+            read_x(t + 1, 0, ax0);
+            if constexpr (decltype(kind)::load) load_x(t + 4);
+            dequant(nx1, 0, bw0);
+#pragma unroll
+            for (int m = 0; m < FM * FN; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // one MFMA
+                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // a fragment read
+                if (m < 2) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);    // a load
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);    // its share of the VALU
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
+    using Full = WideStep<true, true, 2 * kTallLoads>;
+    // Four sub-steps per iteration, no exit between them; of the last four only the first issues
+    // loads (the weights of the last sub-step), their waits count down, and the ones past nt only
+    // wait and sync.
     int t = 0;
-    for (; t + 3 <= nsteps; t += 3) {
-        step(t, r0, 0, r2, 2);
-        step(t + 1, r1, 1, r0, 0);
-        step(t + 2, r2, 2, r1, 1);
+    for (; t + 4 < nt; t += 4) {
+        step(t, r0, r1, r3, Full{});
+        step(t + 1, r1, r2, r0, Full{});
+        step(t + 2, r2, r3, r1, Full{});
+        step(t + 3, r3, r0, r2, Full{});
     }
-    if (t < nsteps) step(t, r0, 0, r2, 2);
-    if (t + 1 < nsteps) step(t + 1, r1, 1, r0, 0);
-    wait_vmcnt<0>();
+    step(t, r0, r1, r3, WideStep<false, true, 2 * kTallLoads>{});
+    step(t + 1, r1, r2, r0, WideStep<false, false, kTallLoads, true>{});
+    step(t + 2, r2, r3, r1, WideStep<false, false, 0, true>{});
+    step(t + 3, r3, r0, r2, WideStep<false, false, 0, true>{});
 
-    // Output: accumulator (i, j, r) of lane l is row 16i + 4(l / 16) + r, column 64w + 16j + l % 16.
-    // Each wave stages its 64 columns in its own LDS area, 64 rows at a time in output layout,
-    // and writes 8 outputs per lane and store (16 bytes). The block barrier frees the activation
-    // buffers; after it each wave reads back only what it wrote.
+    // Each wave's 128 x 32 block -> LDS (once every wave is done with the activation buffers and
+    // every direct load has landed) -> 16-byte stores of 8 outputs (y or the split-K partials).
+    wait_vmcnt<0>();
     __syncthreads();
-    constexpr int P = out_pitch(kBigFN);  // 68 floats
-    float* stage = reinterpret_cast<float*>(lds) + wid * 64 * P;
+    float* stage = reinterpret_cast<float*>(lds) + wid * kTallBM * kTallPitch;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) stage[(16 * i + 4 * g + r) * kTallPitch + 16 * j + c] = acc[i][j][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
     const bool vec = out8_vector_ok<YT>(a, part);
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int i = 0; i < kBigFM / 2; ++i)
-#pragma unroll
-            for (int j = 0; j < kBigFN; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) stage[(16 * i + 4 * g + r) * P + 16 * j + c] = acc[4 * half + i][j][r];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int u = lane + 64 * q, row = u >> 3, col = (u & 7) * 8;  // chunk: 8 of the 64 columns
-            const float4 lo = *reinterpret_cast<const float4*>(stage + row * P + col);
-            const float4 hi = *reinterpret_cast<const float4*>(stage + row * P + col + 4);
-            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            const int m = m0 + 64 * half + row;
-            if (m < a.M) store_out8<YT>(a, part, vec, m, n0 + 64 * wid + col, v);
-        }
+    for (int k = 0; k < kTallBM * 4 / 64; ++k) {
+        const int u = lane + 64 * k;  // chunk of 8 outputs: row u / 4, columns 8 (u % 4)
+        const int row = u >> 2, col = (u & 3) * 8;
+        const int m = m0 + row;
+        float v[8];
+        const float* src = stage + row * kTallPitch + col;
+        const float4 s0 = *reinterpret_cast<const float4*>(src);
+        const float4 s1 = *reinterpret_cast<const float4*>(src + 4);
+        v[0] = s0.x; v[1] = s0.y; v[2] = s0.z; v[3] = s0.w;
+        v[4] = s1.x; v[5] = s1.y; v[6] = s1.z; v[7] = s1.w;
+        if (m < a.M) store_out8<YT>(a, part, vec, m, col0 + col, v);
     }
 }
 
@@ -1426,29 +1458,29 @@ bool q4_wide_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 128) * a.row_bytes < kLim && (uint64_t)(a.N + 128) * a.gpr * 2 < kLim;
 }
 
-// Whether the large-tile kernel takes the call: the pipelined kernel's conditions, K % 128 == 0 and
-// all operand offsets, with the rows and columns a tile reaches past M and N, below 2^31.
+// Whether the 128 x 256 tile (the tall kernel) takes the call: the wide tile's conditions (the
+// prefill copy among them), with the rows and columns a 128 x 256 tile reaches past M and N.
 bool q4_big_ok(const GemmArgs& a) {
     constexpr uint64_t kLim = 0x80000000u;
-    return a.K % 128 == 0 && q4_pipe_ok(a) && (uint64_t)(a.M + kBigM) * a.K * 2 < kLim &&
-           (uint64_t)(a.N + kBigN) * a.row_bytes < kLim && (uint64_t)(a.N + kBigN) * a.gpr * 2 < kLim;
+    return q4_wide_ok(a) && (uint64_t)(a.M + kTallBM) * a.K * 2 < kLim && (uint64_t)(a.N + kTallBN) * a.row_bytes < kLim;
 }
 
 int q4_big_splits(const GemmArgs& a);
 
-// The large tile with one block per CU, K split as q4_big_splits says (or `split_choice`).
+// The 128 x 256 tile (the tall kernel) with one block per CU, K split as q4_big_splits says (or
+// `split_choice`).
 void launch_q4_big(const GemmArgs& a0, int split_choice = 0) {
     GemmArgs a = a0;
-    const long tiles = (long)((a.N + kBigN - 1) / kBigN) * ((a.M + kBigM - 1) / kBigM);
-    const int nsteps = a.K / 128;
-    const int splits = choose_split(a, tiles, nsteps, 4, split_choice > 0 ? split_choice : q4_big_splits(a));
-    const dim3 grid((a.N + kBigN - 1) / kBigN, (a.M + kBigM - 1) / kBigM, splits);
+    const long tiles = (long)((a.N + kTallBN - 1) / kTallBN) * ((a.M + kTallBM - 1) / kTallBM);
+    const int forced = split_choice > 0 ? split_choice : q4_big_splits(a);
+    const int splits = choose_split(a, tiles, a.K / kWideSub, 8, forced);
+    const dim3 grid((a.N + kTallBN - 1) / kTallBN, (a.M + kTallBM - 1) / kTallBM, splits);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL(q4_gemm_big<BYHIP_F32>, grid, dim3(256), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL(q4_gemm_big<BYHIP_F16>, grid, dim3(256), 0, stream(), a); break;
-    default: hipLaunchKernelGGL(q4_gemm_big<BYHIP_BF16>, grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F32: hipLaunchKernelGGL(q4_gemm_tall<BYHIP_F32>, grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL(q4_gemm_tall<BYHIP_F16>, grid, dim3(512), 0, stream(), a); break;
+    default: hipLaunchKernelGGL(q4_gemm_tall<BYHIP_BF16>, grid, dim3(512), 0, stream(), a); break;
     }
-    BYHIP_LAUNCHED("q4_gemm_big");
+    BYHIP_LAUNCHED("q4_gemm_tall");
     if (a.part) launch_splitk_sum(a, splits);
 }
 
@@ -1513,26 +1545,28 @@ bool q4_small_wide(const GemmArgs& a) {
 }
 
 // Splits launch_q4_big chooses: K is split when the tiles fill at most half the CUs, into as many
-// slices as keep the grid within one block per CU (each slice at least 4 steps).
+// slices as keep the grid within one block per CU (each slice at least 8 sub-steps).
 int q4_big_splits(const GemmArgs& a) {
-    const long tiles = (long)((a.N + kBigN - 1) / kBigN) * ((a.M + kBigM - 1) / kBigM);
+    const long tiles = (long)((a.N + kTallBN - 1) / kTallBN) * ((a.M + kTallBM - 1) / kTallBM);
     const int forced = env_int("BYHIP_Q4_SPLIT", 0);
     if (forced > 0) return forced;
-    return (int)std::max<long>(1, std::min<long>(compute_units() / tiles, a.K / 128 / 4));
+    return (int)std::max<long>(1, std::min<long>(compute_units() / tiles, a.K / kWideSub / 8));
 }
 
 // The Q4 prefill kernel (M above the skinny kernel's range) for the benchmark format, from
-// measurements on MI355X:
+// measurements on MI355X (c4's projections, weights streamed from HBM):
 //   the 64 x 128 wide tile when its tiles alone fill the CUs while 128 x 256 tiles would leave
-//   more than half of them idle (M = 512, N = K = 4096: 25 us against 38 us);
-//   else, for M > 64, the 128 x 256 tile, which reads about half the operand bytes per output,
-//   unless the split-K it needs to fill the CUs moves partial sums (8 bytes per output and split:
-//   written, then read) of more than 100 bytes per tile and K value. At M = 256 it wins on
-//   gate+up (no split: 76 us against 103 us) and loses on down (K = 14336, 8 splits: 52.0 us
-//   against 47.4), o (N = K = 4096: 30.3 against 22.7) and qkv (34.0 against 34.5, even); the wide
-//   tile also takes M <= 64 (half-empty large tiles);
-//   the pipelined kernel where neither takes the call (K % 128 != 0, offsets past 2^31).
-// BYHIP_Q4_PREFILL forces one: 1 the pipelined kernel, 2 the large tile, 3 the wide tile,
+//   more than half of them idle (M = 512, N = K = 4096: 20.6 us against 31.0 for the 128 x 256
+//   tile split 4 ways);
+//   else, for M > 64, the 128 x 256 tile (the tall kernel), which reads about half the operand
+//   bytes per output, unless the split-K it needs to fill the CUs moves partial sums (8 bytes per
+//   output and split: written, then read) of more than 100 bytes per tile and K value. It wins on
+//   gate+up (K = 4096, N = 28672) at M = 256 (no split: 55 against 80 us) and M = 512 (110
+//   against 142), and loses at M = 256 on qkv (N = 6144: 26.7 against 17.7), o (26.4 against
+//   20.4) and down (K = 14336: 41.6 against 36.6), and at M = 128 on all four; the wide tile also
+//   takes M <= 64 (half-empty large tiles);
+//   the pipelined kernel where neither takes the call (no prefill copy, offsets past 2^31).
+// BYHIP_Q4_PREFILL forces one: 1 the pipelined kernel, 2 the 128 x 256 tile, 3 the wide tile,
 // when it takes the call. Returns kQ4Pipe / kQ4Big / kQ4Wide, or 0 for the general kernel.
 int q4_prefill_kind(const GemmArgs& a) {
     const int forced = env_int("BYHIP_Q4_PREFILL", 0);
@@ -1541,7 +1575,7 @@ int q4_prefill_kind(const GemmArgs& a) {
     if (forced == 2 && big) return kQ4Big;
     if (forced == 3 && wide) return kQ4Wide;
     const long cus = compute_units();
-    const long big_tiles = (long)((a.N + kBigN - 1) / kBigN) * ((a.M + kBigM - 1) / kBigM);
+    const long big_tiles = (long)((a.N + kTallBN - 1) / kTallBN) * ((a.M + kTallBM - 1) / kTallBM);
     const long wide_tiles = (long)((a.N + 127) / 128) * ((a.M + 63) / 64);
     if (wide && wide_tiles >= cus && 2 * big_tiles < cus) return kQ4Wide;
     if (big && (a.M > 64 || !wide)) {
