@@ -20,6 +20,7 @@
 // hi*w_lo keep the fp32 weight, so fp32 activations meet the reference's fp32 tolerance. fp16
 // activations are used as they are, against the weight rounded once to fp16.
 #include <algorithm>
+#include <utility>
 
 #include "byhip_gemm.h"
 #include "byhip_internal.h"
@@ -815,15 +816,15 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   at slot c ^ ((r / 2) % 8): the fragment reads (16 rows, one chunk each) then hit 16 distinct
 //   bank groups. Four buffers per group.
 //   Sub-step t of a group runs in two halves around one block barrier: the kk = 0 MFMAs beside
-//   the dequantization of the kk = 1 weights and the weight loads of t + 3 (into the register set
-//   t - 1 finished with); the wait for this wave's loads of t + 1 and the barrier (which publishes
-//   every wave's direct loads of t + 1 and, since each wave's fragment reads of t have returned,
-//   frees buffer t % 4); the kk = 1 MFMAs beside the fragment reads of t + 1, the dequantization
-//   of t + 1's kk = 0 weights and the activation loads of t + 4 into buffer t % 4. The
-//   dequantization VALU work thus runs between MFMAs of the same wave (interleaved by scheduling
-//   groups), the loads are spread over both halves (8 % faster at K = 14336 than all in the
-//   second), and loads have two and a half to three and a half
-//   sub-steps to land. Every group runs the same number of sub-steps (the barrier needs the same
+//   the fragment reads of t's kk = 1 activations, the dequantization of t's kk = 1 weights and the
+//   loads of t + 3 (weights into the register set t - 1 finished with, activations into buffer
+//   (t + 3) % 4, whose reads of t - 1 all returned before the previous barrier); the wait for this
+//   wave's loads of t + 1 and the barrier (which publishes every wave's direct loads of t + 1); the
+//   kk = 1 MFMAs beside the fragment reads of t + 1's kk = 0 activations and the dequantization of
+//   t + 1's kk = 0 weights. The dequantization VALU work thus runs between MFMAs of the same wave
+//   (interleaved by scheduling groups), and loads have two and a half sub-steps to land. With the
+//   loads of a sub-step split over both halves and all fragment reads in the second, the kernel was
+//   6 % slower at K = 14336. Every group runs the same number of sub-steps (the barrier needs the same
 //   count in every wave), the largest group's; a sub-step past a group's last reads zeros through
 //   an out-of-range offset and adds nothing. The last one to four sub-steps issue no loads (their
 //   waits count down instead).
@@ -857,13 +858,12 @@ struct WideW {
     v2u s;
 };
 
-// A sub-step's kind: whether it issues activation loads (of 4 sub-steps ahead) and weight loads
-// (of 3 ahead), how many of this wave's loads may stay in flight at its mid-step wait, and whether
-// it may lie past the last sub-step (then it only waits and syncs).
-template <bool L, bool LW, int W, bool G = false>
+// A sub-step's kind: whether it issues the loads of the sub-step a pipeline depth minus one ahead,
+// how many of this wave's loads may stay in flight at its mid-step wait, and whether it may lie
+// past the last sub-step (then it only waits and syncs).
+template <bool L, int W, bool G = false>
 struct WideStep {
     static constexpr bool load = L;
-    static constexpr bool load_ws = LW;
     static constexpr int wait = W;
     static constexpr bool guard = G;
 };
@@ -966,12 +966,11 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             bw[j] = *reinterpret_cast<const h8*>(&u);
         }
     };
-    auto read_x = [&](int t, h8 (&x0)[FM], h8 (&x1)[FM]) {
-        const uint8_t* src = xgrp + (t & 3) * kXBuf;
+    // The kk half of sub-step t's activation fragments.
+    auto read_x = [&](int t, int kk, h8 (&x)[FM]) {
+        const uint8_t* src = xgrp + (t & 3) * kXBuf + (kk ? rd1 : rd0);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) x0[i] = *reinterpret_cast<const h8*>(src + 2048 * i + rd0);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) x1[i] = *reinterpret_cast<const h8*>(src + 2048 * i + rd1);
+        for (int i = 0; i < FM; ++i) x[i] = *reinterpret_cast<const h8*>(src + 2048 * i);
     };
     auto mfmas = [&](const h8 (&x)[FM], const h8 (&b)[FN]) {
 #pragma unroll
@@ -981,8 +980,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
     };
 
-    // Issue order: sub-step t's activations, then its weights (t = 0, 1, 2), and sub-step 3's
-    // activations; sub-step 3's weights follow in sub-step 0.
+    // Sub-steps 0, 1, 2 are loaded here (activations, then weights), sub-step t + 3 in sub-step t.
     WideW r0, r1, r2, r3;
     h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
     load_x(0);
@@ -991,31 +989,34 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     load_ws(r1, 1);
     load_x(2);
     load_ws(r2, 2);
-    load_x(3);
-    wait_vmcnt<2 * kLoads + FM>();
+    wait_vmcnt<2 * kLoads>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    read_x(0, ax0, ax1);
+    read_x(0, 0, ax0);
     dequant(r0, 0, bw0);
 
     // Sub-step t with register sets cur (t's operands), nx1 (t + 1's) and nx3 (refilled with t + 3's
-    // weights in the first half, once cur's last fragments are dequantized: the loads stay spread
-    // over both halves). The second half issues t + 4's activations into buffer t % 4. At the
+    // weights, once cur's last fragments are dequantized); t + 3's activations go to buffer
+    // (t + 3) % 4, which every wave's reads of t - 1 freed before the previous barrier. At the
     // mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
     constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
-    auto step = [&](int t, WideW& cur, const WideW& nx1, WideW& nx3, auto kind) {
-        constexpr bool kLoad = decltype(kind)::load;
+    auto step = [&](int t, const WideW& cur, const WideW& nx1, WideW& nx3, auto kind) {
         constexpr int kWait = decltype(kind)::wait;
         const bool live = !decltype(kind)::guard || t < nt_all;
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax0, bw0);
+            read_x(t, 1, ax1);
             dequant(cur, 1, bw1);
-            if constexpr (decltype(kind)::load_ws) load_ws(nx3, t + 3);
+            if constexpr (decltype(kind)::load) {
+                load_ws(nx3, t + 3);
+                load_x(t + 3);
+            }
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                          // one MFMA
-                if (m < FN + 1) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);         // a load
-                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);               // its share of the VALU
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                        // one MFMA
+                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);            // a fragment read
+                if (m < kLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);        // a load
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);             // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1023,24 +1024,19 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
-            h8 x1c[FM];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) x1c[i] = ax1[i];
-            mfmas(x1c, bw1);
-            read_x(t + 1, ax0, ax1);
-            if constexpr (kLoad) load_x(t + 4);
+            mfmas(ax1, bw1);
+            read_x(t + 1, 0, ax0);
             dequant(nx1, 0, bw0);
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
-                if (m < 2 * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // a fragment read
-                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);       // a load
-                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);        // its share of the VALU
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // one MFMA
+                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // a fragment read
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);    // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    using Full = WideStep<true, true, 2 * kLoads>;
+    using Full = WideStep<true, 2 * kLoads>;
     // Four sub-steps per iteration and no exit between them (an exit there made the register
     // allocator keep extra copies of the accumulators and spill). Of the last four only the first
     // issues loads (the weights of the last sub-step); the loads of the sub-steps up to 3 past them
@@ -1053,10 +1049,10 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         step(t + 2, r2, r3, r1, Full{});
         step(t + 3, r3, r0, r2, Full{});
     }
-    step(t, r0, r1, r3, WideStep<false, true, 2 * kLoads>{});
-    step(t + 1, r1, r2, r0, WideStep<false, false, kLoads, true>{});
-    step(t + 2, r2, r3, r1, WideStep<false, false, 0, true>{});
-    step(t + 3, r3, r0, r2, WideStep<false, false, 0, true>{});
+    step(t, r0, r1, r3, WideStep<true, 2 * kLoads>{});
+    step(t + 1, r1, r2, r0, WideStep<false, kLoads, true>{});
+    step(t + 2, r2, r3, r1, WideStep<false, 0, true>{});
+    step(t + 3, r3, r0, r2, WideStep<false, 0, true>{});
 
     // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
     // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
@@ -1108,13 +1104,12 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
 //   for a sub-step are two 8-byte loads and its 2 fragments' scales one 4-byte load; the block's
 //   activation slice (128 rows x 128 bytes, 16 KB) moves straight into LDS, each wave loading 16
 //   rows, XOR-swizzled as in the wide tile. Four buffers.
-//   Sub-step t runs in two halves around one block barrier: the kk = 0 MFMAs beside the fragment
-//   reads of t's kk = 1 activations, the dequantization of t's kk = 1 weights and the weight loads
-//   of t + 3; the wait for this wave's loads of t + 1 and the barrier (which publishes every wave's
-//   direct loads of t + 1 and, every wave's reads of t having returned, frees buffer t % 4); the
-//   kk = 1 MFMAs beside the reads of t + 1's kk = 0 activations, the dequantization of t + 1's
-//   kk = 0 weights and the activation loads of t + 4 into buffer t % 4. The last four sub-steps
-//   issue no activation loads, and those past the last only wait and sync.
+//   Sub-step t runs in two halves around one block barrier, as in the wide tile: the kk = 0 MFMAs
+//   beside the fragment reads of t's kk = 1 activations, the dequantization of t's kk = 1 weights
+//   and the loads of t + 3; the wait for this wave's loads of t + 1 and the barrier; the kk = 1
+//   MFMAs beside the reads of t + 1's kk = 0 activations and the dequantization of t + 1's kk = 0
+//   weights. Of the last four sub-steps only the first issues loads, and those past the last only
+//   wait and sync. (Six or eight buffers, loads five or seven sub-steps ahead: no faster.)
 //   Output: each wave stages its 128 x 32 block in LDS (rows of 36 floats: the accumulator writes
 //   hit 64 distinct banks) and writes it as 16-byte stores of 8 outputs; no cross-wave sums.
 //   Split-K: block z covers the sub-steps [z * split_steps, ...) and writes fp32 partials.
@@ -1122,9 +1117,19 @@ constexpr int kTallBM = 128, kTallBN = 256;
 constexpr int kTallXBuf = kTallBM * kWideSub * 2;           // one activation buffer (16 KB)
 constexpr int kTallLoads = 2 + 2 + 1;                       // loads per wave and sub-step
 constexpr int kTallPitch = 32 + 4;                          // floats per row of a wave's staged block
-constexpr int kTallLdsX = 4 * kTallXBuf;
 constexpr int kTallLdsOut = 8 * kTallBM * kTallPitch * 4;  // the eight waves' staged blocks
-constexpr int kTallLds = kTallLdsX > kTallLdsOut ? kTallLdsX : kTallLdsOut;
+constexpr int kTallDepth = 4;                               // activation buffers and operand sets
+constexpr int tall_lds(int depth) { return depth * kTallXBuf > kTallLdsOut ? depth * kTallXBuf : kTallLdsOut; }
+
+// Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // One wave's prefill-copy operands of one sub-step: per fragment 16 nibbles (two words), and the
 // two fragments' fp16 scales.
@@ -1133,10 +1138,11 @@ struct TallW {
     uint32_t s;
 };
 
-template <int YT>
+template <int YT, int D = kTallDepth>
 __global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
+    static_assert(D >= 3 && D * kTallXBuf <= 160 * 1024, "q4_gemm_tall: 3 to 10 buffers");
     constexpr int FM = 8, FN = 2;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kTallLds];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[tall_lds(D)];
 
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, g = lane >> 4;
@@ -1174,12 +1180,12 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
     const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
 
     // Loads of sub-step t (the sub-step's offset in the scalar offset; past the last, 2^31 there
-    // reads zeros): its activations into buffer t % 4, its weights and scales into a register set.
-    auto load_x = [&](int t) {
+    // reads zeros): its activations into buffer t % D, its weights and scales into a register set.
+    auto load_x = [&](int t, int buf) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
-        uint8_t* const dst = lds + (t & 3) * kTallXBuf;
+        uint8_t* const dst = lds + buf * kTallXBuf;
 #pragma unroll
         for (int q = 0; q < 2; ++q) lds_dma16(xr, dst + 1024 * (2 * wid + q), xo[q], oob + 128u * u);
     };
@@ -1221,9 +1227,9 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
             bw[j] = *reinterpret_cast<const h8*>(&u);
         }
     };
-    // The kk half of sub-step t's activation fragments.
-    auto read_x = [&](int t, int kk, h8 (&x)[FM]) {
-        const uint8_t* src = lds + (t & 3) * kTallXBuf + (kk ? rd1 : rd0);
+    // The kk half of the activation fragments in buffer buf.
+    auto read_x = [&](int buf, int kk, h8 (&x)[FM]) {
+        const uint8_t* src = lds + buf * kTallXBuf + (kk ? rd1 : rd0);
 #pragma unroll
         for (int i = 0; i < FM; ++i) x[i] = *reinterpret_cast<const h8*>(src + 2048 * i);
     };
@@ -1235,40 +1241,45 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
     };
 
-    // Issue order: sub-step t's activations, then its weights (t = 0, 1, 2), and sub-step 3's
-    // activations; sub-step 3's weights follow in sub-step 0.
-    TallW r0, r1, r2, r3;
+    // Sub-steps 0 .. D - 2 are loaded here (activations, then weights), sub-step t + D - 1 in
+    // sub-step t.
+    TallW rs[D];
     h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
-    load_x(0);
-    load_ws(r0, 0);
-    load_x(1);
-    load_ws(r1, 1);
-    load_x(2);
-    load_ws(r2, 2);
-    load_x(3);
-    wait_vmcnt<2 * kTallLoads + 2>();
+    static_for<D - 1>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        load_x(k, k);
+        load_ws(rs[k], k);
+    });
+    wait_vmcnt<(D - 2) * kTallLoads>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read_x(0, 0, ax0);
-    dequant(r0, 0, bw0);
+    dequant(rs[0], 0, bw0);
 
     constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
-    // Sub-step t with register sets cur (t's operands), nx1 (t + 1's) and nx3 (refilled with t + 3's
-    // weights); at the mid-step wait the loads of t + 2 and t + 3 may stay in flight, those issued.
-    auto step = [&](int t, const TallW& cur, const TallW& nx1, TallW& nx3, auto kind) {
+    // Sub-step t = base + k (base a multiple of D) with register sets rs[k] (t's operands),
+    // rs[k + 1] (t + 1's) and rs[k - 1] (refilled with t + D - 1's weights), all indices mod D;
+    // t + D - 1's activations go to buffer k - 1, which every wave's reads of t - 1 freed before the
+    // previous barrier. At the mid-step wait the loads of t + 2 .. t + D - 1 may stay in flight,
+    // those issued.
+    auto step = [&](int t, auto kc, auto kind) {
+        constexpr int k = decltype(kc)::value, k1 = (k + 1) % D, kp = (k + D - 1) % D;
         constexpr int kWait = decltype(kind)::wait;
         const bool live = !decltype(kind)::guard || t < nt;
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax0, bw0);
-            read_x(t, 1, ax1);
-            dequant(cur, 1, bw1);
-            if constexpr (decltype(kind)::load_ws) load_ws(nx3, t + 3);
+            read_x(k, 1, ax1);
+            dequant(rs[k], 1, bw1);
+            if constexpr (decltype(kind)::load) {
+                load_ws(rs[kp], t + D - 1);
+                load_x(t + D - 1, kp);
+            }
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
-                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);       // a fragment read
-                if (m < FN + 1) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
-                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);        // its share of the VALU
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                       // one MFMA
+                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);           // a fragment read
+                if (m < kTallLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);  // a load
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);            // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1277,34 +1288,27 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax1, bw1);
-            read_x(t + 1, 0, ax0);
-            if constexpr (decltype(kind)::load) load_x(t + 4);
-            dequant(nx1, 0, bw0);
+            read_x(k1, 0, ax0);
+            dequant(rs[k1], 0, bw0);
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
                 __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // one MFMA
                 if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // a fragment read
-                if (m < 2) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);    // a load
                 __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);    // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    using Full = WideStep<true, true, 2 * kTallLoads>;
-    // Four sub-steps per iteration, no exit between them; of the last four only the first issues
-    // loads (the weights of the last sub-step), their waits count down, and the ones past nt only
-    // wait and sync.
+    // D sub-steps per iteration, no exit between them; of the last D only the first issues loads
+    // (the weights of the last sub-step), their waits count down, and the ones past nt only wait
+    // and sync.
     int t = 0;
-    for (; t + 4 < nt; t += 4) {
-        step(t, r0, r1, r3, Full{});
-        step(t + 1, r1, r2, r0, Full{});
-        step(t + 2, r2, r3, r1, Full{});
-        step(t + 3, r3, r0, r2, Full{});
-    }
-    step(t, r0, r1, r3, WideStep<false, true, 2 * kTallLoads>{});
-    step(t + 1, r1, r2, r0, WideStep<false, false, kTallLoads, true>{});
-    step(t + 2, r2, r3, r1, WideStep<false, false, 0, true>{});
-    step(t + 3, r3, r0, r2, WideStep<false, false, 0, true>{});
+    for (; t + D < nt; t += D)
+        static_for<D>([&](auto kc) { step(t + decltype(kc)::value, kc, WideStep<true, (D - 2) * kTallLoads>{}); });
+    static_for<D>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        step(t + k, kc, WideStep<k == 0, (D - 2 - k > 0 ? D - 2 - k : 0) * kTallLoads, (k > 0)>{});
+    });
 
     // Each wave's 128 x 32 block -> LDS (once every wave is done with the activation buffers and
     // every direct load has landed) -> 16-byte stores of 8 outputs (y or the split-K partials).
