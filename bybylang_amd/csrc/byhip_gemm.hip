@@ -920,11 +920,14 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // (FM direct loads), its weights and scales into a register set (5 loads); the sub-step's offset
     // goes in the scalar offset. A sub-step past the group's last (t >= nt) adds 2^31 there, which
     // every resource rejects: it reads zeros without touching memory.
-    auto load_x = [&](int t) {
+    // Buffer indices are compile-time constants at every call (t % 4 in the unrolled loop): the
+    // compiler then sees that reads of one buffer do not alias direct loads into another and waits
+    // for no direct load before them (with a run-time index it waited for nearly all in flight).
+    auto load_x = [&](int t, int buf) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
-        uint8_t* const dst = xgrp + (t & 3) * kXBuf;
+        uint8_t* const dst = xgrp + buf * kXBuf;
 #pragma unroll
         for (int q = 0; q < FM; ++q) lds_dma16(xr, dst + 1024 * (FM * h + q), xo[q], oob + 128u * u);
     };
@@ -966,9 +969,9 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             bw[j] = *reinterpret_cast<const h8*>(&u);
         }
     };
-    // The kk half of sub-step t's activation fragments.
-    auto read_x = [&](int t, int kk, h8 (&x)[FM]) {
-        const uint8_t* src = xgrp + (t & 3) * kXBuf + (kk ? rd1 : rd0);
+    // The kk half of the activation fragments in buffer buf.
+    auto read_x = [&](int buf, int kk, h8 (&x)[FM]) {
+        const uint8_t* src = xgrp + buf * kXBuf + (kk ? rd1 : rd0);
 #pragma unroll
         for (int i = 0; i < FM; ++i) x[i] = *reinterpret_cast<const h8*>(src + 2048 * i);
     };
@@ -983,11 +986,11 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // Sub-steps 0, 1, 2 are loaded here (activations, then weights), sub-step t + 3 in sub-step t.
     WideW r0, r1, r2, r3;
     h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
-    load_x(0);
+    load_x(0, 0);
     load_ws(r0, 0);
-    load_x(1);
+    load_x(1, 1);
     load_ws(r1, 1);
-    load_x(2);
+    load_x(2, 2);
     load_ws(r2, 2);
     wait_vmcnt<2 * kLoads>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -999,17 +1002,18 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // (t + 3) % 4, which every wave's reads of t - 1 freed before the previous barrier. At the
     // mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
     constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
-    auto step = [&](int t, const WideW& cur, const WideW& nx1, WideW& nx3, auto kind) {
+    auto step = [&](int t, auto kc, const WideW& cur, const WideW& nx1, WideW& nx3, auto kind) {
+        constexpr int k = decltype(kc)::value;  // t % 4
         constexpr int kWait = decltype(kind)::wait;
         const bool live = !decltype(kind)::guard || t < nt_all;
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax0, bw0);
-            read_x(t, 1, ax1);
+            read_x(k, 1, ax1);
             dequant(cur, 1, bw1);
             if constexpr (decltype(kind)::load) {
                 load_ws(nx3, t + 3);
-                load_x(t + 3);
+                load_x(t + 3, (k + 3) % 4);
             }
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
@@ -1025,7 +1029,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax1, bw1);
-            read_x(t + 1, 0, ax0);
+            read_x((k + 1) % 4, 0, ax0);
             dequant(nx1, 0, bw0);
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
@@ -1043,16 +1047,20 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // are in flight (those past nt_all read zeros), and their waits count down; the ones past
     // nt_all only wait and sync.
     int t = 0;
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
+    using K2 = std::integral_constant<int, 2>;
+    using K3 = std::integral_constant<int, 3>;
     for (; t + 4 < nt_all; t += 4) {
-        step(t, r0, r1, r3, Full{});
-        step(t + 1, r1, r2, r0, Full{});
-        step(t + 2, r2, r3, r1, Full{});
-        step(t + 3, r3, r0, r2, Full{});
+        step(t, K0{}, r0, r1, r3, Full{});
+        step(t + 1, K1{}, r1, r2, r0, Full{});
+        step(t + 2, K2{}, r2, r3, r1, Full{});
+        step(t + 3, K3{}, r3, r0, r2, Full{});
     }
-    step(t, r0, r1, r3, WideStep<true, 2 * kLoads>{});
-    step(t + 1, r1, r2, r0, WideStep<false, kLoads, true>{});
-    step(t + 2, r2, r3, r1, WideStep<false, 0, true>{});
-    step(t + 3, r3, r0, r2, WideStep<false, 0, true>{});
+    step(t, K0{}, r0, r1, r3, WideStep<true, 2 * kLoads>{});
+    step(t + 1, K1{}, r1, r2, r0, WideStep<false, kLoads, true>{});
+    step(t + 2, K2{}, r2, r3, r1, WideStep<false, 0, true>{});
+    step(t + 3, K3{}, r3, r0, r2, WideStep<false, 0, true>{});
 
     // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
     // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
