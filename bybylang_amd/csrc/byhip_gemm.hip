@@ -814,20 +814,20 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   Activations: the group's sub-step slice (64 rows x 128 bytes, one line per row) moves straight
 //   from global memory into LDS, each wave of the group loading 32 rows, 16-byte chunk c of row r
 //   at slot c ^ ((r / 2) % 8): the fragment reads (16 rows, one chunk each) then hit 16 distinct
-//   bank groups. Four buffers per group.
+//   bank groups. D buffers per group (wide_depth).
 //   Sub-step t of a group runs in two halves around one block barrier: the kk = 0 MFMAs beside
 //   the fragment reads of t's kk = 1 activations, the dequantization of t's kk = 1 weights and the
-//   loads of t + 3 (weights into the register set t - 1 finished with, activations into buffer
-//   (t + 3) % 4, whose reads of t - 1 all returned before the previous barrier); the wait for this
+//   loads of t + D - 1 (weights into the register set t - 1 finished with, activations into buffer
+//   (t - 1) % D, whose reads of t - 1 all returned before the previous barrier); the wait for this
 //   wave's loads of t + 1 and the barrier (which publishes every wave's direct loads of t + 1); the
 //   kk = 1 MFMAs beside the fragment reads of t + 1's kk = 0 activations and the dequantization of
 //   t + 1's kk = 0 weights. The dequantization VALU work thus runs between MFMAs of the same wave
-//   (interleaved by scheduling groups), and loads have two and a half sub-steps to land. With the
+//   (interleaved by scheduling groups), and loads have D - 1.5 sub-steps to land. With the
 //   loads of a sub-step split over both halves and all fragment reads in the second, the kernel was
 //   6 % slower at K = 14336. Every group runs the same number of sub-steps (the barrier needs the same
 //   count in every wave), the largest group's; a sub-step past a group's last reads zeros through
-//   an out-of-range offset and adds nothing. The last one to four sub-steps issue no loads (their
-//   waits count down instead).
+//   an out-of-range offset and adds nothing. The last D - 1 sub-steps issue no loads (their waits
+//   count down instead).
 //   Tile order: with the tile count a multiple of 8, the workgroups that share an XCD (every 8th
 //   workgroup id) take a contiguous run of tiles in groups of 4 row tiles, so each XCD's L2 holds
 //   the activations of 4 row tiles and the weights of the column tiles it needs, rather than
@@ -837,19 +837,33 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   group order (0 + 1 + 2 + 3) and writes them with 16-byte stores.
 constexpr int kWideBN = 128;
 constexpr int kWideSub = 64;                         // K values per sub-step
-constexpr int kWideDepth = 4;                        // activation buffers per group
 constexpr int kWidePitch = out_pitch(kWideBN / 16);  // floats per row of a staged partial tile
 
-// Sizes for FM row fragments (BM = 16 FM rows: 64 for prefill, 32 or 16 for small M).
-template <int FM>
+// Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Sizes for FM row fragments (BM = 16 FM rows: 64 for prefill, 32 or 16 for small M) and D
+// activation buffers per group (loads D - 1 sub-steps ahead).
+template <int FM, int D>
 struct WideShape {
     static constexpr int kBM = 16 * FM;
     static constexpr int kXBuf = kBM * kWideSub * 2;          // one activation buffer
     static constexpr int kLoads = FM + 4 + 1;                 // loads per wave and sub-step
-    static constexpr int kLdsX = 4 * kWideDepth * kXBuf;      // 4 groups x 4 buffers
+    static constexpr int kLdsX = 4 * D * kXBuf;               // 4 groups x D buffers
     static constexpr int kLdsRed = 4 * kBM * kWidePitch * 4;  // 4 partial tiles
     static constexpr int kLds = kLdsX > kLdsRed ? kLdsX : kLdsRed;
 };
+// Pipeline depth (activation buffers per group): four at every tile height. Deeper pipelines were
+// slower at 32 rows (c4's M = 32 gate+up: 17.1 us with four buffers, 18.8 with five or six, 19.6
+// with eight; qkv 10.0, 10.7, 11.2, 12.1).
+constexpr int wide_depth(int) { return 4; }
 
 // One wave's prefill-copy operands of one sub-step: per fragment 16 nibbles (two words), and the
 // four fragments' fp16 scales.
@@ -868,12 +882,14 @@ struct WideStep {
     static constexpr bool guard = G;
 };
 
-template <int FM, int YT>
+template <int FM, int YT, int D = wide_depth(FM)>
 __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     static_assert(FM == 1 || FM == 2 || FM == 4, "q4_gemm_wide: 16, 32 or 64 rows");
     constexpr int FN = 4;
-    using S = WideShape<FM>;
+    using S = WideShape<FM, D>;
     constexpr int BM = S::kBM, kXBuf = S::kXBuf, kLoads = S::kLoads;
+    static_assert(D >= 4 && S::kLds <= 160 * 1024 && (D - 2) * kLoads <= 63,
+                  "q4_gemm_wide: the buffers must fit LDS and the loads in flight the wait counter");
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
 
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -911,16 +927,16 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     const uint32_t wfrag = nsub_all * 512u;  // per fragment
     const uint32_t wo = (uint32_t)(n0 + 64 * h) / 16u * wfrag + 8u * lane;
     const uint32_t so = (uint32_t)(n0 + 64 * h) / 64u * nsub_all * 256u + 8u * (16u * (uint32_t)(g >> 1) + c);
-    uint8_t* const xgrp = lds + p * kWideDepth * kXBuf;  // the group's buffers
+    uint8_t* const xgrp = lds + p * D * kXBuf;  // the group's buffers
     // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot (2 g + kk) ^ (c / 2)
     // ((16 i + c) / 2 % 8 is c / 2): one lane offset per kk, the fragment a constant 2048 i.
     const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
 
-    // The loads of the group's sub-step t (block sub-step p + 4 t): its activations into buffer t % 4
+    // The loads of the group's sub-step t (block sub-step p + 4 t): its activations into buffer t % D
     // (FM direct loads), its weights and scales into a register set (5 loads); the sub-step's offset
     // goes in the scalar offset. A sub-step past the group's last (t >= nt) adds 2^31 there, which
     // every resource rejects: it reads zeros without touching memory.
-    // Buffer indices are compile-time constants at every call (t % 4 in the unrolled loop): the
+    // Buffer indices are compile-time constants at every call (t % D in the unrolled loop): the
     // compiler then sees that reads of one buffer do not alias direct loads into another and waits
     // for no direct load before them (with a run-time index it waited for nearly all in flight).
     auto load_x = [&](int t, int buf) {
@@ -983,37 +999,38 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
     };
 
-    // Sub-steps 0, 1, 2 are loaded here (activations, then weights), sub-step t + 3 in sub-step t.
-    WideW r0, r1, r2, r3;
+    // Sub-steps 0 .. D - 2 are loaded here (activations, then weights), sub-step t + D - 1 in
+    // sub-step t.
+    WideW rs[D];
     h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
-    load_x(0, 0);
-    load_ws(r0, 0);
-    load_x(1, 1);
-    load_ws(r1, 1);
-    load_x(2, 2);
-    load_ws(r2, 2);
-    wait_vmcnt<2 * kLoads>();
+    static_for<D - 1>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        load_x(k, k);
+        load_ws(rs[k], k);
+    });
+    wait_vmcnt<(D - 2) * kLoads>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read_x(0, 0, ax0);
-    dequant(r0, 0, bw0);
+    dequant(rs[0], 0, bw0);
 
-    // Sub-step t with register sets cur (t's operands), nx1 (t + 1's) and nx3 (refilled with t + 3's
-    // weights, once cur's last fragments are dequantized); t + 3's activations go to buffer
-    // (t + 3) % 4, which every wave's reads of t - 1 freed before the previous barrier. At the
-    // mid-step wait the loads of t + 2 and t + 3 may stay in flight, those that were issued.
+    // Sub-step t = base + k (base a multiple of D) with register sets rs[k] (t's operands),
+    // rs[k + 1] (t + 1's) and rs[k - 1] (refilled with t + D - 1's weights, once t's last fragments
+    // are dequantized), all indices mod D; t + D - 1's activations go to buffer k - 1, which every
+    // wave's reads of t - 1 freed before the previous barrier. At the mid-step wait the loads of
+    // t + 2 .. t + D - 1 may stay in flight, those that were issued.
     constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
-    auto step = [&](int t, auto kc, const WideW& cur, const WideW& nx1, WideW& nx3, auto kind) {
-        constexpr int k = decltype(kc)::value;  // t % 4
+    auto step = [&](int t, auto kc, auto kind) {
+        constexpr int k = decltype(kc)::value, k1 = (k + 1) % D, kp = (k + D - 1) % D;
         constexpr int kWait = decltype(kind)::wait;
         const bool live = !decltype(kind)::guard || t < nt_all;
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax0, bw0);
             read_x(k, 1, ax1);
-            dequant(cur, 1, bw1);
+            dequant(rs[k], 1, bw1);
             if constexpr (decltype(kind)::load) {
-                load_ws(nx3, t + 3);
-                load_x(t + 3, (k + 3) % 4);
+                load_ws(rs[kp], t + D - 1);
+                load_x(t + D - 1, kp);
             }
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
@@ -1029,8 +1046,8 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (live) {
             mfmas(ax1, bw1);
-            read_x((k + 1) % 4, 0, ax0);
-            dequant(nx1, 0, bw0);
+            read_x(k1, 0, ax0);
+            dequant(rs[k1], 0, bw0);
 #pragma unroll
             for (int m = 0; m < FM * FN; ++m) {
                 __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // one MFMA
@@ -1040,27 +1057,18 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    using Full = WideStep<true, 2 * kLoads>;
-    // Four sub-steps per iteration and no exit between them (an exit there made the register
-    // allocator keep extra copies of the accumulators and spill). Of the last four only the first
-    // issues loads (the weights of the last sub-step); the loads of the sub-steps up to 3 past them
-    // are in flight (those past nt_all read zeros), and their waits count down; the ones past
+    // D sub-steps per iteration and no exit between them (an exit there made the register
+    // allocator keep extra copies of the accumulators and spill). Of the last D only the first
+    // issues loads (the weights of the last sub-step); the loads of the sub-steps up to D - 1 past
+    // them are in flight (those past nt_all read zeros), and their waits count down; the ones past
     // nt_all only wait and sync.
     int t = 0;
-    using K0 = std::integral_constant<int, 0>;
-    using K1 = std::integral_constant<int, 1>;
-    using K2 = std::integral_constant<int, 2>;
-    using K3 = std::integral_constant<int, 3>;
-    for (; t + 4 < nt_all; t += 4) {
-        step(t, K0{}, r0, r1, r3, Full{});
-        step(t + 1, K1{}, r1, r2, r0, Full{});
-        step(t + 2, K2{}, r2, r3, r1, Full{});
-        step(t + 3, K3{}, r3, r0, r2, Full{});
-    }
-    step(t, K0{}, r0, r1, r3, WideStep<true, 2 * kLoads>{});
-    step(t + 1, K1{}, r1, r2, r0, WideStep<false, kLoads, true>{});
-    step(t + 2, K2{}, r2, r3, r1, WideStep<false, 0, true>{});
-    step(t + 3, K3{}, r3, r0, r2, WideStep<false, 0, true>{});
+    for (; t + D < nt_all; t += D)
+        static_for<D>([&](auto kc) { step(t + decltype(kc)::value, kc, WideStep<true, (D - 2) * kLoads>{}); });
+    static_for<D>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        step(t + k, kc, WideStep<k == 0, (D - 2 - k > 0 ? D - 2 - k : 0) * kLoads, (k > 0)>{});
+    });
 
     // Partial tiles -> LDS in output layout, once every wave's loads have landed (the last ones
     // read zeros into the buffers) and every wave is done with the activation buffers -> sums in
@@ -1128,16 +1136,6 @@ constexpr int kTallPitch = 32 + 4;                          // floats per row of
 constexpr int kTallLdsOut = 8 * kTallBM * kTallPitch * 4;  // the eight waves' staged blocks
 constexpr int kTallDepth = 4;                               // activation buffers and operand sets
 constexpr int tall_lds(int depth) { return depth * kTallXBuf > kTallLdsOut ? depth * kTallXBuf : kTallLdsOut; }
-
-// Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // One wave's prefill-copy operands of one sub-step: per fragment 16 nibbles (two words), and the
 // two fragments' fp16 scales.
