@@ -6,6 +6,7 @@ fp16, meets the fp32-accumulate tier (max-abs-rel <= 1e-3); fp16 outputs are com
 oracle's values are rounded the same way. Unpacked codes and scales are bit-exact.
 """
 import os
+import zlib
 
 import numpy as np
 import pytest
@@ -300,7 +301,8 @@ def test_q4_layer_down_auto_split(hip, oracle, M):
                                   "f32_scales", "odd_k", "gpr_pad", "k32"])
 @pytest.mark.parametrize("M", [1, 3, 24])
 def test_q4_edge_shapes(hip, oracle, case, M):
-    r = np.random.default_rng(hash(case) % 1000 + M)
+    # a seed that does not depend on the process (str hashes are salted per process)
+    r = np.random.default_rng(zlib.crc32(case.encode()) % 1000 + M)
     K, N, grp = 256, 72, 32
     if case == "group0":
         grp = 0
