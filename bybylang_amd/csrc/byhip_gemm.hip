@@ -812,9 +812,9 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 //   Weights: per fragment and sub-step a lane's 16 nibbles are 8 contiguous bytes of a 512-byte
 //   block, so a load touches whole lines; its four fragments' scales are one 8-byte load.
 //   Activations: the group's sub-step slice (64 rows x 128 bytes, one line per row) moves straight
-//   from global memory into LDS, each wave of the group loading 32 rows, 16-byte chunk c of row r
-//   at slot c ^ ((r / 2) % 8): the fragment reads (16 rows, one chunk each) then hit 16 distinct
-//   bank groups. D buffers per group (wide_depth).
+//   from global memory into LDS, each wave of the group loading 32 rows, 16-byte chunk k of row r
+//   at slot k ^ x_swizzle(r), so the fragment reads (16 rows, one chunk each) are free of bank
+//   conflicts. D buffers per group (wide_depth).
 //   Sub-step t of a group runs in two halves around one block barrier: the kk = 0 MFMAs beside
 //   the fragment reads of t's kk = 1 activations, the dequantization of t's kk = 1 weights and the
 //   loads of t + D - 1 (weights into the register set t - 1 finished with, activations into buffer
@@ -838,6 +838,18 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 constexpr int kWideBN = 128;
 constexpr int kWideSub = 64;                         // K values per sub-step
 constexpr int kWidePitch = out_pitch(kWideBN / 16);  // floats per row of a staged partial tile
+
+// LDS slot swizzle of the activation slices (rows of 128 bytes, eight 16-byte chunks): chunk k of
+// row r sits at slot k ^ x_swizzle(r). The fragment reads (lane (c, g) reads chunk 2 g + kk of row
+// 16 i + c, 16 bytes) are then free of bank conflicts: measured on the MI355X, a ds_read_b128 is
+// served 32 lanes at a time and conflicts when two of them hit the same 16-byte unit modulo 32
+// (128 banks of 4 bytes); with rows 128 bytes apart, lanes c and c + 4 share that unit unless their
+// slots differ, so bits 2 and 3 of the row pick the slot's bits 0 and 2 (bit 1 of the row its bit
+// 1). Measured standalone: 2.3-2.5 ns per wave-wide read per CU, as fast as contiguous reads,
+// against 3.7-4.0 with the slot k ^ (r / 2 % 8) used before (4 conflict cycles per read).
+__host__ __device__ constexpr int x_swizzle(int r) {
+    return ((r >> 2) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+}
 
 // Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order.
 template <typename F, int... I>
@@ -921,16 +933,17 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     uint32_t xo[FM];
 #pragma unroll
     for (int q = 0; q < FM; ++q) {
-        const int r = 8 * FM * h + 8 * q + (lane >> 3), chunk = (lane & 7) ^ ((r >> 1) & 7);
+        const int r = 8 * FM * h + 8 * q + (lane >> 3), chunk = (lane & 7) ^ x_swizzle(r);
         xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
     const uint32_t wfrag = nsub_all * 512u;  // per fragment
     const uint32_t wo = (uint32_t)(n0 + 64 * h) / 16u * wfrag + 8u * lane;
     const uint32_t so = (uint32_t)(n0 + 64 * h) / 64u * nsub_all * 256u + 8u * (16u * (uint32_t)(g >> 1) + c);
     uint8_t* const xgrp = lds + p * D * kXBuf;  // the group's buffers
-    // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot (2 g + kk) ^ (c / 2)
-    // ((16 i + c) / 2 % 8 is c / 2): one lane offset per kk, the fragment a constant 2048 i.
-    const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
+    // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot
+    // (2 g + kk) ^ x_swizzle(c) (x_swizzle(16 i + c) is x_swizzle(c)): one lane offset per kk, the
+    // fragment a constant 2048 i.
+    const int rd0 = 128 * c + 16 * ((2 * g) ^ x_swizzle(c)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ x_swizzle(c));
 
     // The loads of the group's sub-step t (block sub-step p + 4 t): its activations into buffer t % D
     // (FM direct loads), its weights and scales into a register set (5 loads); the sub-step's offset
@@ -1176,14 +1189,14 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_tall(GemmArgs a) {
     uint32_t xo[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        const int r = 16 * wid + 8 * q + (lane >> 3), chunk = (lane & 7) ^ ((r >> 1) & 7);
+        const int r = 16 * wid + 8 * q + (lane >> 3), chunk = (lane & 7) ^ x_swizzle(r);
         xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
     const uint32_t wfrag = nsub_all * 512u;  // per fragment
     const uint32_t wo = (uint32_t)col0 / 16u * wfrag + 8u * lane;
     // the wave's 2 fragments are fragments 2 (w % 2) and 2 (w % 2) + 1 of their quad
     const uint32_t so = (uint32_t)col0 / 64u * nsub_all * 256u + 8u * (16u * (uint32_t)(g >> 1) + c) + 4u * (wid & 1);
-    const int rd0 = 128 * c + 16 * ((2 * g) ^ (c >> 1)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ (c >> 1));
+    const int rd0 = 128 * c + 16 * ((2 * g) ^ x_swizzle(c)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ x_swizzle(c));
 
     // Loads of sub-step t (the sub-step's offset in the scalar offset; past the last, 2^31 there
     // reads zeros): its activations into buffer t % D, its weights and scales into a register set.
