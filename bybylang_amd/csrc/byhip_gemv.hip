@@ -98,8 +98,12 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * R);
     const bool rows_live = n0 < N;  // uniform in the wave; every wave takes part in the barrier
 
-    uint32_t* xh = lds;                                   // [M][G][16] fp16 pairs
-    uint32_t* xl = xh + M * G * 16;                       // [M][G][16] low terms (fp32 x only)
+    // Staged chunk idx (= m G + chunk) as four 16-byte pieces, piece t at uint4 index t M G + idx:
+    // a wave's reads of piece t (64 consecutive chunks) and the staging writes then hit consecutive
+    // 16-byte units, free of LDS bank conflicts (with the chunk's 64 bytes contiguous, four lanes
+    // shared each unit modulo 32: four passes per read).
+    uint32_t* xh = lds;                                   // [4][M][G][4] fp16 pairs
+    uint32_t* xl = xh + M * G * 16;                       // [4][M][G][4] low terms (fp32 x only)
     float* sums = reinterpret_cast<float*>(xl + (XS == 2 ? M * G * 16 : 0));  // [M][G]{bias, sum}
 
     const rsrc_t wr = make_rsrc(a.wq, (uint32_t)N * (uint32_t)a.row_bytes);
@@ -244,13 +248,13 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
                 s = sl + sh;
                 bias = 1024.0f * sl + 64.0f * sh;
             }
-            uint4* dh = reinterpret_cast<uint4*>(xh + idx * 16);
+            uint4* dh = reinterpret_cast<uint4*>(xh) + idx;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) dh[t] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
+            for (int t = 0; t < 4; ++t) dh[t * M * G] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
             if constexpr (XS == 2) {
-                uint4* dl = reinterpret_cast<uint4*>(xl + idx * 16);
+                uint4* dl = reinterpret_cast<uint4*>(xl) + idx;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) dl[t] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
+                for (int t = 0; t < 4; ++t) dl[t * M * G] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
             }
             sums[2 * idx] = bias;
             sums[2 * idx + 1] = s;
@@ -267,17 +271,17 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     float bias[M][CPL], sx[M][CPL];
     auto read_x = [&](int m, int c, uint32_t* hp, uint32_t* lp) {
         const int idx = m * G + (int)(coff[c] >> 4);
-        const uint4* sh = reinterpret_cast<const uint4*>(xh + idx * 16);
+        const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const uint4 u = sh[t];
+            const uint4 u = sh[t * M * G];
             hp[4 * t] = u.x; hp[4 * t + 1] = u.y; hp[4 * t + 2] = u.z; hp[4 * t + 3] = u.w;
         }
         if constexpr (XS == 2) {
-            const uint4* sl = reinterpret_cast<const uint4*>(xl + idx * 16);
+            const uint4* sl = reinterpret_cast<const uint4*>(xl) + idx;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const uint4 u = sl[t];
+                const uint4 u = sl[t * M * G];
                 lp[4 * t] = u.x; lp[4 * t + 1] = u.y; lp[4 * t + 2] = u.z; lp[4 * t + 3] = u.w;
             }
         }
@@ -452,8 +456,10 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int K = a.K, G = K >> 5;
-    uint32_t* xh = lds;                                      // [G][16] fp16 pairs, high terms
-    uint32_t* xl = xh + G * 16;                              // [G][16] low terms
+    // chunk idx as four 16-byte pieces, piece t at uint4 index t G + idx (conflict-free reads, as
+    // in q4_gemv)
+    uint32_t* xh = lds;                                      // [4][G][4] fp16 pairs, high terms
+    uint32_t* xl = xh + G * 16;                              // [4][G][4] low terms
     float* sums = reinterpret_cast<float*>(xl + G * 16);     // [G] sum of the scaled x over the chunk
     float* facs = sums + G;                                  // [G] the chunk's back-scale 2^-sh
     float* ssq_part = facs + G;                              // [256]
@@ -581,12 +587,12 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
         float s = 0.0f;
 #pragma unroll
         for (int t = 0; t < 32; ++t) s += v[t];
-        uint4* dh = reinterpret_cast<uint4*>(xh + idx * 16);
-        uint4* dl = reinterpret_cast<uint4*>(xl + idx * 16);
+        uint4* dh = reinterpret_cast<uint4*>(xh) + idx;
+        uint4* dl = reinterpret_cast<uint4*>(xl) + idx;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            dh[t] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
-            dl[t] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
+            dh[t * G] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
+            dl[t * G] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
         }
         sums[idx] = s;
         facs[idx] = __builtin_amdgcn_ldexpf(1.0f, -sh);
@@ -626,11 +632,11 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
         for (int c = 0; c < CPL; ++c) {
             const int idx = (int)(coff[c] >> 4);
             uint32_t xp[16], xq[16];
-            const uint4* sh = reinterpret_cast<const uint4*>(xh + idx * 16);
-            const uint4* sl = reinterpret_cast<const uint4*>(xl + idx * 16);
+            const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
+            const uint4* sl = reinterpret_cast<const uint4*>(xl) + idx;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const uint4 u = sh[t], w = sl[t];
+                const uint4 u = sh[t * G], w = sl[t * G];
                 xp[4 * t] = u.x; xp[4 * t + 1] = u.y; xp[4 * t + 2] = u.z; xp[4 * t + 3] = u.w;
                 xq[4 * t] = w.x; xq[4 * t + 1] = w.y; xq[4 * t + 2] = w.z; xq[4 * t + 3] = w.w;
             }
