@@ -548,11 +548,21 @@ __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part
 //   so every product pairs the same k.
 //   Activations: each wave moves its step's BM x 128 slice straight from global memory into its
 //   own LDS buffer (16 lanes read a row's 256 bytes, so every load is a run of whole lines), with
-//   16-byte chunk c of row r at slot c ^ (r & 15): the fragment reads (16 rows, one chunk each)
-//   then hit 16 distinct bank groups. Each wave reads only what it loaded, so no barrier is
+//   16-byte chunk c of row r at slot c ^ skinny_swizzle(r), so the fragment reads (16 rows, one
+//   chunk each) are free of bank conflicts. Each wave reads only what it loaded, so no barrier is
 //   needed; the double buffer and a vmcnt wait order the direct loads and the reads.
 //   Shapes: BM x 16 FN with FN = 4 column fragments and BM 16 or 32 (two blocks per CU). The
 //   64 x 128 prefill tile with the same operand layout is q4_gemm_wide.
+// LDS slot swizzle of the skinny kernel's activation rows (256 bytes, sixteen 16-byte chunks):
+// chunk k of row r sits at slot k ^ skinny_swizzle(r). A ds_read_b128 is served 32 lanes at a time
+// and conflicts when two of them hit the same 16-byte unit modulo 32 (128 banks of 4 bytes,
+// measured on the MI355X); rows 256 bytes apart fall on units 16 (r % 2) + slot, and this swizzle
+// (row bits 1, 2, 3 into slot bits 0, 1, 3) keeps the 32 lanes of a fragment read (16 rows, two
+// chunks) on 32 distinct units. The slot k ^ (r % 16) used before put two lanes on each unit.
+__host__ __device__ constexpr int skinny_swizzle(int r) {
+    return ((r >> 1) & 1) | (((r >> 2) & 1) << 1) | (((r >> 3) & 1) << 3);
+}
+
 template <int FN>
 struct SkinnyW {
     v4u w[FN];       // 32 nibbles of one column per fragment
@@ -640,13 +650,13 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
                            : make_rsrc(a.scales, (uint32_t)((size_t)a.N * a.gpr * 2));
     const int gshift = a.group ? __builtin_ctz((unsigned)a.group >> 5) : 0;
     // Direct load u of a step: lane -> row 4u + lane / 16, LDS slot lane % 16 holding chunk
-    // slot ^ (row & 15) of that row. Loads u and u + 4 differ by 16 rows and share the slot
+    // slot ^ skinny_swizzle(row) of that row. Loads u and u + 4 differ by 16 rows and share the slot
     // pattern, so four lane offsets serve them all; the rest of every offset is wave-uniform and
     // travels in the scalar offset, as does each column fragment's row of weights and scales.
     uint32_t xo[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int r = 4 * q + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+        const int r = 4 * q + (lane >> 4), chunk = (lane & 15) ^ skinny_swizzle(r);
         xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
     const uint32_t xrow16 = 16u * (uint32_t)K * 2u;  // 16 activation rows
@@ -711,7 +721,7 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
         auto xread = [&](int kk) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                xv[kk % XA][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ c));
+                xv[kk % XA][i] = *reinterpret_cast<const uint4*>(src + 256 * (16 * i + c) + 16 * ((4 * g + kk) ^ skinny_swizzle(c)));
         };
 #pragma unroll
         for (int kk = 0; kk < XA; ++kk) xread(kk);
