@@ -30,7 +30,11 @@ namespace byhip {
 namespace {
 
 constexpr int BM = 64, BN = 128, BK = 64;
-constexpr int LDA = BK + 8;  // halves per LDS row (16-byte pad)
+// Halves per LDS row: 160 bytes, 10 16-byte units, so that the fragment reads (lanes 0..15 on
+// rows 0..15 at one 16-byte unit, lanes 16..31 one unit further) fall on 32 distinct units modulo
+// 32, which a ds_read_b128 serves in one pass (with a 16-byte pad, 144-byte rows, two lanes
+// shared a unit).
+constexpr int LDA = BK + 16;
 
 template <BFormat F>
 struct FormatTraits {
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(256) void row_range_shift(const float* __restrict__
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 constexpr int PBK = 64;
-constexpr int PLD = PBK + 8;  // halves per LDS row (16-byte pad: conflict-free operand reads)
+constexpr int PLD = PBK + 16;  // halves per LDS row (160-byte rows: conflict-free fragment reads, as LDA)
 
 template <int BM, int BN>
 struct PipeShape {
