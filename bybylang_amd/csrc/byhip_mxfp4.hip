@@ -60,14 +60,9 @@ struct MxArgs {
 // LDS layout.
 //   Data regions (2), each two K steps e, e + 1 (e even) of the 256 x rows (32 KB) then the 256 W
 //   rows. Rows come in blocks of 8 (1 KB): step e's 64 bytes of each row in the first 512 bytes,
-//   step e + 1's in the second, row r of the block at 64 (r % 8) + 16 (c ^ swz(r % 32)) for K
-//   block c. A direct load (8 lanes per row: 4 per step half) fills one block. The MFMA operand
-//   reads (lanes 0..31 and 32..63 each read 16 bytes of 32 neighbouring rows) are free of bank
-//   conflicts: measured on the MI355X, a ds_read_b128 is served 32 lanes at a time and conflicts
-//   when two of them hit the same 16-byte unit modulo 32 (128 banks of 4 bytes). Rows r and r + 8,
-//   r + 16, r + 24 sit at the same unit modulo 32 unless their slots differ, so the slot takes
-//   bits 3 and 4 of the row (the slot from bits 0..3 used before left rows r and r + 16 on one
-//   unit: 2 passes per read).
+//   step e + 1's in the second, row r of the block at 64 (r % 8) + 16 (c ^ swz(r % 16)) for K
+//   block c. A direct load (8 lanes per row: 4 per step half) fills one block, and the swizzle
+//   makes the MFMA operand reads, 16 neighbouring rows per 16 lanes, free of bank conflicts.
 //   Scale buffers (2), one per 4-step period: 256 x rows of 16 bytes, then 256 W rows; byte 4 t + c
 //   of a row is the scale of block c of step t of the period (the row's 16 scale bytes in memory).
 //   After the K loop the regions hold the output tile on its way to global memory.
@@ -82,7 +77,7 @@ constexpr int kPairDma = 16;                                 // direct loads per
 constexpr int kOutPitch = 128 + 8;                           // floats per staged output row
 constexpr int kOutWaveBytes = 32 * kOutPitch * 4;            // 32 rows per wave and pass
 
-__device__ __forceinline__ int swz(int r) { return (r >> 3) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 2)) & 3; }
 
 // One wave's operands of one K step: 4 x fragments and 4 W fragments of 32 rows, each as two
 // 64-deep halves, and per fragment the scale bytes of both halves (bytes 0 and 1 of one register,
@@ -148,7 +143,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         const int R = 64 * wid + 8 * q + drow;  // tile row
-        const uint32_t c = 16u * (uint32_t)((lane & 3) ^ swz(R & 31)) + 64u * (uint32_t)(lane >> 5);
+        const uint32_t c = 16u * (uint32_t)((lane & 3) ^ swz(R & 15)) + 64u * (uint32_t)(lane >> 5);
         xo[q] = (uint32_t)(m0 + R) * kb + c;
         wo[q] = (uint32_t)(n0 + R) * kb + c;
     }
@@ -185,7 +180,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemm(MxArgs a) {
     int rd[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-        rd[h] = kGroupBytes * ((lane & 31) >> 3) + 64 * (lane & 7) + 16 * ((2 * lq + h) ^ swz(lane & 31));
+        rd[h] = kGroupBytes * ((lane & 31) >> 3) + 64 * (lane & 7) + 16 * ((2 * lq + h) ^ swz(lane & 15));
     const int sa_row = 16 * (128 * wm + (lane & 31)) + 2 * lq;
     const int sb_row = kScaleOpBytes + 16 * (128 * wn + (lane & 31)) + 2 * lq;
     auto read_frag = [&](Frags& f, const uint8_t* stage, int op, int F, int h) {
