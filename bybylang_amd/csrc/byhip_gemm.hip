@@ -242,7 +242,10 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
 
     const int arow = tid >> 2, aseg = tid & 3;
     const int bcol = tid >> 1, bhalf = tid & 1;
-    for (int k0 = 0; k0 < a.K; k0 += BK) {
+    // split-K: block z covers the K steps [z * split_steps, (z + 1) * split_steps)
+    const int k_begin = a.part ? (int)blockIdx.z * a.split_steps * BK : 0;
+    const int k_end = a.part ? min(a.K, k_begin + a.split_steps * BK) : a.K;
+    for (int k0 = k_begin; k0 < k_end; k0 += BK) {
         stage_a<PERM, XF32>(a, m0 + arow, k0, aseg, &As[arow * LDA + 16 * aseg],
                             XF32 ? &Al[arow * LDA + 16 * aseg] : nullptr);
         stage_b<F, WLO>(a, n0 + bcol, k0 + 32 * bhalf, lut_s, &Bs[bcol * LDA + 32 * bhalf],
@@ -278,6 +281,7 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
         __syncthreads();
     }
 
+    float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -290,7 +294,8 @@ __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
                     // fp32 activations: undo the row's shift (exact unless the result over- or
                     // underflows, as the reference's own sum would)
                     const float v = XF32 ? __builtin_amdgcn_ldexpf(acc[i][j][r], -a.row_shift[m]) : acc[i][j][r];
-                    store_y<YT>(a.y, (size_t)m * a.N + n, v);
+                    if (part) part[(size_t)m * a.N + n] = v;
+                    else store_y<YT>(a.y, (size_t)m * a.N + n, v);
                 }
             }
         }
@@ -1609,8 +1614,13 @@ int q4_prefill_kind(const GemmArgs& a) {
 }
 
 template <BFormat F, bool XF32>
-void launch_fx(const GemmArgs& a) {
-    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+void launch_fx(const GemmArgs& a0) {
+    // K split (fp32 partial sums, added by splitk_sum) when the tiles leave CUs idle: at M = 16,
+    // K = N = 4096 the 32 tiles alone keep 32 of the 256 CUs busy
+    GemmArgs a = a0;
+    const long tiles = (long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+    const int splits = choose_split(a, tiles, (a.K + BK - 1) / BK, 8, 0, 1);
+    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
     case BYHIP_F32:
         hipLaunchKernelGGL((gemm_f16_mfma<F, XF32, BYHIP_F32>), grid, dim3(256), 0, stream(), a);
@@ -1623,6 +1633,7 @@ void launch_fx(const GemmArgs& a) {
         break;
     }
     BYHIP_LAUNCHED("gemm_f16_mfma");
+    if (a.part) launch_splitk_sum(a, splits);
 }
 
 template <BFormat F>
@@ -1641,6 +1652,10 @@ void launch_f(const GemmArgs& a0) {
                        shifts);
     BYHIP_LAUNCHED("row_range_shift");
     a.row_shift = shifts;
+    // the split-K partial sums, if any, go after the shifts
+    const size_t used = ((size_t)a.M * sizeof(int) + 255) / 256 * 256;
+    a.work = static_cast<uint8_t*>(work) + used;
+    a.work_bytes = work_bytes > used ? work_bytes - used : 0;
     launch_fx<F, true>(a);
 }
 
