@@ -141,6 +141,29 @@ def test_gemm_fp32_activations_wide_range(hip, oracle, M, weights):
     ref_check(got, oracle.matmul_q4(x.reshape(-1), wq, sc, ze, M, K, N, 32, K // 32))
 
 
+@pytest.mark.parametrize("splits", ["", "1", "2", "5"])
+@pytest.mark.parametrize("M", [9, 40])
+def test_gemm_fp32_activations_split_k(hip, oracle, monkeypatch, M, splits):
+    """The same GEMM on a long K with few tiles, where it splits K (fp32 partial sums added by
+    splitk_sum in slice order): the default split (8 slices of 8 steps here), none, and forced
+    2 and 5 (unequal slices: 64 steps as 13 + 13 + 13 + 13 + 12), fp32 and fp16 outputs, against
+    the oracle at the reference's fp32 tolerance (fp16 outputs after the oracle's own rounding,
+    plus one fp16 step)."""
+    g = synth.rng(7400 + M + 3 * len(splits))
+    K, N = 4096, 384
+    monkeypatch.setenv("BYHIP_Q4_SPLIT", splits)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    ze = g.uniform(6.0, 9.0, size=ze.size).astype(np.float32)  # per-group zeros: the generic kernel
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    x = wide_x(g, M, K, -3.0, 3.0)
+    want = oracle.matmul_q4(x.reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    print(f"gemm fp32 split-K M={M} splits={splits or 'default'}", flush=True)
+    ref_check(run_q4(hip, x, hip.F32, w, M, N), want)
+    got16 = run_q4(hip, x, hip.F32, w, M, N, hip.F16)
+    # both roundings to fp16 may land one fp16 step apart: at most 2^-10 of the peak
+    ref_check(got16, np.asarray(want, np.float32).astype(np.float16).astype(np.float32), REF_TOL + 2.0 ** -10)
+
+
 @pytest.mark.parametrize("scales", ["tiny", "huge", "mixed"])
 @pytest.mark.parametrize("M", [3, 40])
 def test_q4_scales_outside_fp16(hip, oracle, M, scales):
