@@ -52,6 +52,9 @@ struct GemmArgs {
     // Set by the fp32-activation launch of the fp16 MFMA kernel: per-row exponents t (x * 2^t is
     // split into fp16 hi + lo; the row's sums are scaled by 2^-t).
     const int* row_shift = nullptr;
+    // The wide tile on fp32 activations: x holds the high fp16 plane of the shifted activations and
+    // x_lo the low one (x * 2^t = hi + lo, t per row in row_shift).
+    const void* x_lo = nullptr;
 };
 
 // Floats between consecutive split-K partials (16-byte aligned).

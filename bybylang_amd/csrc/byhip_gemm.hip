@@ -316,6 +316,46 @@ __global__ __launch_bounds__(256) void row_range_shift(const float* __restrict__
     if (threadIdx.x == 0) out[blockIdx.x] = fp16_range_shift(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])));
 }
 
+// fp32 activations for the wide tile: the row's shift t as row_range_shift finds it, and the
+// shifted row as two fp16 planes, hi = fp16(x 2^t) and lo = fp16(x 2^t - hi) (about 22 bits of x).
+// One block per row, K % 4 == 0, 16-byte aligned rows.
+__global__ __launch_bounds__(256) void split_rows_f16(const float* __restrict__ x, int K, int* __restrict__ shifts,
+                                                     _Float16* __restrict__ hi, _Float16* __restrict__ lo) {
+    __shared__ float part[4];
+    __shared__ int shift;
+    const size_t row = (size_t)blockIdx.x * K;
+    const float4* r = reinterpret_cast<const float4*>(x + row);
+    float mx = 0.0f;
+    for (int k = threadIdx.x; k < K / 4; k += 256) {
+        const float4 v = r[k];
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        shift = fp16_range_shift(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])));
+        shifts[blockIdx.x] = shift;
+    }
+    __syncthreads();
+    const int t = shift;
+    for (int k = threadIdx.x; k < K / 4; k += 256) {
+        const float4 v = r[k];
+        const float s[4] = {__builtin_amdgcn_ldexpf(v.x, t), __builtin_amdgcn_ldexpf(v.y, t),
+                            __builtin_amdgcn_ldexpf(v.z, t), __builtin_amdgcn_ldexpf(v.w, t)};
+        uint16_t h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const _Float16 he = (_Float16)s[e];
+            h[e] = h_bits(he);
+            l[e] = h_bits((_Float16)(s[e] - (float)he));
+        }
+        reinterpret_cast<uint2*>(hi + row)[k] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+        reinterpret_cast<uint2*>(lo + row)[k] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    }
+}
+
 // Pipelined Q4 GEMM for the benchmark format: fp16 activations, fp16 scales, one integral zero,
 // group 0 or 32 * 2^j, K % 64 == 0. A 256-thread block computes a BM x BN tile (BM 32 or 64, BN 64
 // or 128, chosen per shape) in K steps of 64 (two 32-value groups); its four waves each own a
@@ -864,13 +904,14 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Sizes for FM row fragments (BM = 16 FM rows: 64 for prefill, 32 or 16 for small M) and D
-// activation buffers per group (loads D - 1 sub-steps ahead).
-template <int FM, int D>
+// Sizes for FM row fragments (BM = 16 FM rows: 64 for prefill, 32 or 16 for small M), D
+// activation buffers per group (loads D - 1 sub-steps ahead) and XS activation planes (1: fp16
+// activations; 2: fp32 activations as a high and a low fp16 plane).
+template <int FM, int D, int XS = 1>
 struct WideShape {
     static constexpr int kBM = 16 * FM;
-    static constexpr int kXBuf = kBM * kWideSub * 2;          // one activation buffer
-    static constexpr int kLoads = FM + 4 + 1;                 // loads per wave and sub-step
+    static constexpr int kXBuf = XS * kBM * kWideSub * 2;     // one activation buffer (all planes)
+    static constexpr int kLoads = XS * FM + 4 + 1;            // loads per wave and sub-step
     static constexpr int kLdsX = 4 * D * kXBuf;               // 4 groups x D buffers
     static constexpr int kLdsRed = 4 * kBM * kWidePitch * 4;  // 4 partial tiles
     static constexpr int kLds = kLdsX > kLdsRed ? kLdsX : kLdsRed;
@@ -897,11 +938,12 @@ struct WideStep {
     static constexpr bool guard = G;
 };
 
-template <int FM, int YT, int D = wide_depth(FM)>
+template <int FM, int YT, int D = wide_depth(FM), int XS = 1>
 __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     static_assert(FM == 1 || FM == 2 || FM == 4, "q4_gemm_wide: 16, 32 or 64 rows");
+    static_assert(XS == 1 || (XS == 2 && FM <= 2), "q4_gemm_wide: two activation planes up to 32 rows");
     constexpr int FN = 4;
-    using S = WideShape<FM, D>;
+    using S = WideShape<FM, D, XS>;
     constexpr int BM = S::kBM, kXBuf = S::kXBuf, kLoads = S::kLoads;
     static_assert(D >= 4 && S::kLds <= 160 * 1024 && (D - 2) * kLoads <= 63,
                   "q4_gemm_wide: the buffers must fit LDS and the loads in flight the wait counter");
@@ -929,10 +971,11 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // Rows past M and columns past N read zeros through the range checks (the launcher keeps the
     // offsets below 2^31; the prefill copy pads N to whole fragments).
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
+    const rsrc_t xlr = make_rsrc(XS == 2 ? a.x_lo : a.x, XS == 2 ? (uint32_t)((size_t)a.M * K * 2) : 0u);
     const rsrc_t wr = make_rsrc(a.wpf, (uint32_t)(((size_t)a.N + 15) / 16 * nsub_all * 512));
     const rsrc_t sr = make_rsrc(a.spf, (uint32_t)(((size_t)a.N + 63) / 64 * nsub_all * 256));
     // Direct load q (0 .. FM - 1) of wave h: rows 8 FM h + 8 q + lane / 8 of the tile, LDS slot
-    // lane % 8.
+    // lane % 8 (with two planes, the low plane's rows follow the high plane's in the buffer).
     uint32_t xo[FM];
 #pragma unroll
     for (int q = 0; q < FM; ++q) {
@@ -952,18 +995,24 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // (FM direct loads), its weights and scales into a register set (5 loads); the sub-step's offset
     // goes in the scalar offset. A sub-step past the group's last (t >= nt) adds 2^31 there, which
     // every resource rejects: it reads zeros without touching memory.
+    // The lambdas are always inlined: left to the inliner, the 32-row tile on two activation
+    // planes kept its operand arrays in scratch memory.
     // Buffer indices are compile-time constants at every call (t % D in the unrolled loop): the
     // compiler then sees that reads of one buffer do not alias direct loads into another and waits
     // for no direct load before them (with a run-time index it waited for nearly all in flight).
-    auto load_x = [&](int t, int buf) {
+    auto load_x = [&](int t, int buf) __attribute__((always_inline)) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
         uint8_t* const dst = xgrp + buf * kXBuf;
 #pragma unroll
         for (int q = 0; q < FM; ++q) lds_dma16(xr, dst + 1024 * (FM * h + q), xo[q], oob + 128u * u);
+        if constexpr (XS == 2) {
+#pragma unroll
+            for (int q = 0; q < FM; ++q) lds_dma16(xlr, dst + 128 * BM + 1024 * (FM * h + q), xo[q], oob + 128u * u);
+        }
     };
-    auto load_ws = [&](WideW& r, int t) {
+    auto load_ws = [&](WideW& r, int t) __attribute__((always_inline)) {
         const bool ok = t < nt;
         const uint32_t u = (uint32_t)(s_first + (ok ? p + 4 * t : 0));
         const uint32_t oob = ok ? 0u : 0x80000000u;
@@ -985,40 +1034,61 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Weights of MFMA kk of a sub-step: (q - zero) * scale in fp16, exact in the subtraction.
-    auto dequant = [&](const WideW& r, int kk, h8 (&bw)[FN]) {
+    // Weights of MFMA kk of a sub-step: (q - zero) * scale in fp16, exact in the subtraction. With
+    // two activation planes also the weight's low term: the product (q - zero) * scale has at most
+    // 15 significant bits, so hi = fp16 of it (one rounding) and lo = fma(q - zero, scale, -hi),
+    // which an fp16 holds exactly, add up to it: plane [1] of bw.
+    auto dequant = [&](const WideW& r, int kk, h8 (&bw)[XS][FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const _Float16 sc = bits_h((uint16_t)(r.s[j >> 1] >> (16 * (j & 1))));
             const h2 ss = {sc, sc};
             const uint32_t d = r.w[j][kk], d8 = d >> 8;
-            const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo);
-            const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi);
-            const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo);
-            const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi);
-            const uint4 u = make_uint4(h2_bits((q0 - zz_lo) * ss), h2_bits((q1 - zz_hi) * ss),
-                                       h2_bits((q2 - zz_lo) * ss), h2_bits((q3 - zz_hi) * ss));
-            bw[j] = *reinterpret_cast<const h8*>(&u);
+            const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo) - zz_lo;
+            const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi) - zz_hi;
+            const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo) - zz_lo;
+            const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi) - zz_hi;
+            const h2 w0 = q0 * ss, w1 = q1 * ss, w2 = q2 * ss, w3 = q3 * ss;
+            const uint4 u = make_uint4(h2_bits(w0), h2_bits(w1), h2_bits(w2), h2_bits(w3));
+            bw[0][j] = *reinterpret_cast<const h8*>(&u);
+            if constexpr (XS == 2) {
+                const uint4 l = make_uint4(h2_bits(__builtin_elementwise_fma(q0, ss, -w0)),
+                                           h2_bits(__builtin_elementwise_fma(q1, ss, -w1)),
+                                           h2_bits(__builtin_elementwise_fma(q2, ss, -w2)),
+                                           h2_bits(__builtin_elementwise_fma(q3, ss, -w3)));
+                bw[XS - 1][j] = *reinterpret_cast<const h8*>(&l);
+            }
         }
     };
-    // The kk half of the activation fragments in buffer buf.
-    auto read_x = [&](int buf, int kk, h8 (&x)[FM]) {
+    // The kk half of the activation fragments in buffer buf (plane [1]: the low plane).
+    auto read_x = [&](int buf, int kk, h8 (&x)[XS][FM]) __attribute__((always_inline)) {
         const uint8_t* src = xgrp + buf * kXBuf + (kk ? rd1 : rd0);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) x[i] = *reinterpret_cast<const h8*>(src + 2048 * i);
+        for (int i = 0; i < FM; ++i) x[0][i] = *reinterpret_cast<const h8*>(src + 2048 * i);
+        if constexpr (XS == 2) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) x[XS - 1][i] = *reinterpret_cast<const h8*>(src + 128 * BM + 2048 * i);
+        }
     };
-    auto mfmas = [&](const h8 (&x)[FM], const h8 (&b)[FN]) {
+    // x . w, and with two planes also x_lo . w_hi and x_hi . w_lo (x_lo . w_lo is below fp32's
+    // resolution of the sum).
+    auto mfmas = [&](const h8 (&x)[XS][FM], const h8 (&b)[XS][FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], b[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[0][i], b[0][j], acc[i][j], 0, 0, 0);
+                if constexpr (XS == 2) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[XS - 1][i], b[0][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[0][i], b[XS - 1][j], acc[i][j], 0, 0, 0);
+                }
+            }
     };
 
     // Sub-steps 0 .. D - 2 are loaded here (activations, then weights), sub-step t + D - 1 in
     // sub-step t.
     WideW rs[D];
-    h8 ax0[FM], ax1[FM], bw0[FN], bw1[FN];
+    h8 ax0[XS][FM], ax1[XS][FM], bw0[XS][FN], bw1[XS][FN];
     static_for<D - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         load_x(k, k);
@@ -1034,8 +1104,9 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // are dequantized), all indices mod D; t + D - 1's activations go to buffer k - 1, which every
     // wave's reads of t - 1 freed before the previous barrier. At the mid-step wait the loads of
     // t + 2 .. t + D - 1 may stay in flight, those that were issued.
-    constexpr int kValuPerMfma = (FN * 14 + FM * FN - 1) / (FM * FN);  // a K half's dequantization
-    auto step = [&](int t, auto kc, auto kind) {
+    constexpr int kMfmas = (XS == 2 ? 3 : 1) * FM * FN;                            // per K half
+    constexpr int kValuPerMfma = (FN * (XS == 2 ? 18 : 14) + kMfmas - 1) / kMfmas;  // a K half's dequantization
+    auto step = [&](int t, auto kc, auto kind) __attribute__((always_inline)) {
         constexpr int k = decltype(kc)::value, k1 = (k + 1) % D, kp = (k + D - 1) % D;
         constexpr int kWait = decltype(kind)::wait;
         const bool live = !decltype(kind)::guard || t < nt_all;
@@ -1049,9 +1120,9 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
                 load_x(t + D - 1, kp);
             }
 #pragma unroll
-            for (int m = 0; m < FM * FN; ++m) {
+            for (int m = 0; m < kMfmas; ++m) {
                 __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                        // one MFMA
-                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);            // a fragment read
+                if (m < XS * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);       // a fragment read
                 if (m < kLoads) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);        // a load
                 __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);             // its share of the VALU
             }
@@ -1065,10 +1136,10 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             read_x(k1, 0, ax0);
             dequant(rs[k1], 0, bw0);
 #pragma unroll
-            for (int m = 0; m < FM * FN; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);               // one MFMA
-                if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // a fragment read
-                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);    // its share of the VALU
+            for (int m = 0; m < kMfmas; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                  // one MFMA
+                if (m < XS * FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0); // a fragment read
+                __builtin_amdgcn_sched_group_barrier(0x0002, kValuPerMfma, 0);       // its share of the VALU
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1121,7 +1192,14 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             v[e + 2] = s0.z + s1.z + s2.z + s3.z;
             v[e + 3] = s0.w + s1.w + s2.w + s3.w;
         }
-        if (m < a.M) store_out8<YT>(a, part, vec, m, n, v);
+        if (m < a.M) {
+            if constexpr (XS == 2) {  // fp32 activations: undo the row's power-of-two shift
+                const int sh = a.row_shift[m];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = __builtin_amdgcn_ldexpf(v[e], -sh);
+            }
+            store_out8<YT>(a, part, vec, m, n, v);
+        }
     }
 }
 
@@ -1384,13 +1462,14 @@ void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
     BYHIP_LAUNCHED("q4_gemm_skinny");
 }
 
-template <int FM>
+template <int FM, int XS = 1>
 void launch_q4_wide_shape(const GemmArgs& a, int splits) {
     const dim3 grid((a.N + kWideBN - 1) / kWideBN, (a.M + 16 * FM - 1) / (16 * FM), splits);
+    constexpr int D = wide_depth(FM);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F32>), grid, dim3(512), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F16>), grid, dim3(512), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_BF16>), grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F32, D, XS>), grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F16, D, XS>), grid, dim3(512), 0, stream(), a); break;
+    default: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_BF16, D, XS>), grid, dim3(512), 0, stream(), a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_wide");
 }
@@ -1570,6 +1649,54 @@ bool q4_small_wide(const GemmArgs& a) {
     return (nsub + splits - 1) / splits >= 16;
 }
 
+// Whether the wide tile takes a call with fp32 activations: the weights' prefill copy (its format
+// conditions), K % 64 == 0, 16-byte aligned activation rows, and the operand offsets below 2^31.
+bool q4_wide_f32_ok(const GemmArgs& a) {
+    constexpr uint64_t kLim = 0x80000000u;
+    return a.x_dtype == BYHIP_F32 && a.wpf && a.spf && a.K % kWideSub == 0 && a.scale_f16 && !a.zeros &&
+           reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && (uint64_t)(a.M + 32) * a.K * 2 < kLim &&
+           (uint64_t)(a.N + 128) * a.row_bytes < kLim && (uint64_t)(a.N + 128) * a.gpr * 2 < kLim;
+}
+
+// The wide tile on fp32 activations: per row a power-of-two shift onto fp16's range and the shifted
+// row as two fp16 planes (split_rows_f16, into the scratch), then the 16- or 32-row tile with three
+// MFMAs per product (hi . w_hi + lo . w_hi + hi . w_lo), every fp32 weight and about 22 bits of
+// each activation kept; K split as for the fp16 tile. False, queueing nothing, when the planes do
+// not fit the scratch.
+bool launch_q4_wide_f32(const GemmArgs& a0, int split_choice = 0) {
+    GemmArgs a = a0;
+    uint8_t* const work = static_cast<uint8_t*>(a.work ? a.work : workspace());
+    const size_t work_bytes = a.work ? a.work_bytes : kWorkspaceBytes;
+    const size_t shift_bytes = ((size_t)a.M * sizeof(int) + 255) / 256 * 256;
+    const size_t plane = ((size_t)a.M * a.K * 2 + 255) / 256 * 256;
+    if (shift_bytes + 2 * plane > work_bytes) return false;
+    int* const shifts = reinterpret_cast<int*>(work);
+    _Float16* const hi = reinterpret_cast<_Float16*>(work + shift_bytes);
+    _Float16* const lo = reinterpret_cast<_Float16*>(work + shift_bytes + plane);
+    hipLaunchKernelGGL(split_rows_f16, dim3((unsigned)a.M), dim3(256), 0, stream(), static_cast<const float*>(a.x), a.K,
+                       shifts, hi, lo);
+    BYHIP_LAUNCHED("split_rows_f16");
+    a.x = hi;
+    a.x_lo = lo;
+    a.row_shift = shifts;
+    a.work = work + shift_bytes + 2 * plane;
+    a.work_bytes = work_bytes - shift_bytes - 2 * plane;
+    const int bm = a.M <= 16 ? 16 : 32;
+    const long tiles = (long)((a.N + kWideBN - 1) / kWideBN) * ((a.M + bm - 1) / bm);
+    const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
+    int splits = choose_split(a, tiles, a.K / kWideSub, 1, forced > 0 ? forced : wide_splits(a, tiles), 1);
+    if (a.part) {
+        // whole rounds of the four groups
+        a.split_steps = (a.split_steps + 3) / 4 * 4;
+        splits = (a.K / kWideSub + a.split_steps - 1) / a.split_steps;
+    }
+    if (splits == 1) a.part = nullptr;
+    if (bm == 16) launch_q4_wide_shape<1, 2>(a, splits);
+    else launch_q4_wide_shape<2, 2>(a, splits);
+    if (a.part) launch_splitk_sum(a, splits);
+    return true;
+}
+
 // Splits launch_q4_big chooses: K is split when the tiles fill at most half the CUs, into as many
 // slices as keep the grid within one block per CU (each slice at least 8 sub-steps).
 int q4_big_splits(const GemmArgs& a) {
@@ -1682,7 +1809,9 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
         launch_q4_big(a, splits);
         return true;
     case kQ4Wide:
-        if (fmt != BFormat::Q4Fast || !q4_wide_ok(a)) return false;
+        if (fmt != BFormat::Q4Fast) return false;
+        if (q4_wide_f32_ok(a)) return launch_q4_wide_f32(a, splits);
+        if (!q4_wide_ok(a)) return false;
         launch_q4_skinny(a, splits, true);
         return true;
     case kQ4General:
@@ -1701,6 +1830,8 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.M > 65535 * BM) fail("byhip: M=%d too large for one launch", a.M);
     switch (fmt) {
     case BFormat::Q4Fast:
+        // fp32 activations: the wide tile on two fp16 planes where the scratch holds them
+        if (q4_wide_f32_ok(a) && env_int("BYHIP_Q4_F32_WIDE", 1) != 0 && launch_q4_wide_f32(a)) break;
         if (q4_skinny_ok(a)) {
             launch_q4_skinny(a, 0, q4_small_wide(a));
             break;

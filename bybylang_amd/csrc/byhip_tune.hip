@@ -210,6 +210,9 @@ std::vector<Candidate> candidates(int mt, int x_dtype) {
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanBig, 0, sp}, 3e-3f});
             for (int sp : {0, 1, 2}) c.push_back({{kPlanWide, 0, sp}, 3e-3f});
         }
+    } else {
+        // fp32 activations: the wide tile on two fp16 planes keeps the fp32 tolerance
+        for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanWide, 0, sp}, 1e-4f});
     }
     c.push_back({{kPlanGemm, 0, 0}, 3e-3f});
     c.push_back({{kPlanExact, 0, 0}, 1e-4f});

@@ -17,7 +17,7 @@ import pytest
 
 from bybylang_amd import synth
 from oracle_lib import OP_Q4_COOP_GEMM, OP_Q4_GEMV, f16_tile_program, q4_blob, shape_op_program
-from parity import REF_TOL, ref_check
+from parity import REF_TOL, bf16_bits_to_f32, f32_to_bf16_rne, ref_check
 
 pytestmark = pytest.mark.gpu
 
@@ -162,6 +162,52 @@ def test_gemm_fp32_activations_split_k(hip, oracle, monkeypatch, M, splits):
     got16 = run_q4(hip, x, hip.F32, w, M, N, hip.F16)
     # both roundings to fp16 may land one fp16 step apart: at most 2^-10 of the peak
     ref_check(got16, np.asarray(want, np.float32).astype(np.float16).astype(np.float32), REF_TOL + 2.0 ** -10)
+
+
+@pytest.mark.parametrize("splits", ["", "1", "3"])
+@pytest.mark.parametrize("M", [9, 16, 17, 40, 130, 512])
+def test_gemm_fp32_activations_wide_tile(hip, oracle, monkeypatch, M, splits):
+    """fp32 activations on weights with a prefill copy (fp16 scales, one zero): the 16- or 32-row
+    wide tile on the activations' two fp16 planes (hi . w_hi + lo . w_hi + hi . w_lo), with the
+    default K split, none, and 3 slices (rounded to whole rounds of the four K groups), ragged N
+    (320 = 2.5 column tiles) and M (17, 130); activations over 1e-8 .. 1e6 against the oracle at
+    the reference's fp32 tolerance, and the same rows with the wide tile switched off
+    (BYHIP_Q4_F32_WIDE=0, the generic GEMM) to the same bar."""
+    g = synth.rng(7500 + M + 7 * len(splits))
+    K, N = 2048, 320
+    monkeypatch.setenv("BYHIP_Q4_SPLIT", splits)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    x = wide_x(g, M, K)
+    want = oracle.matmul_q4(x.reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    print(f"gemm fp32 wide tile M={M} splits={splits or 'default'}", flush=True)
+    ref_check(run_q4(hip, x, hip.F32, w, M, N), want)
+    monkeypatch.setenv("BYHIP_Q4_F32_WIDE", "0")
+    ref_check(run_q4(hip, x, hip.F32, w, M, N), want)
+
+
+@pytest.mark.parametrize("y", ["f16", "bf16"])
+@pytest.mark.parametrize("M", [12, 64])
+def test_gemm_fp32_activations_wide_tile_half_outputs(hip, oracle, M, y):
+    """The fp32-activation wide tile writing fp16 and bf16 outputs: the oracle's fp32 result
+    rounded to the output type, plus one step of that type (both roundings may land a step apart:
+    2^-10 of the peak for fp16, 2^-7 for bf16)."""
+    g = synth.rng(7600 + M)
+    K, N = 4096, 384
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    x = wide_x(g, M, K, -3.0, 3.0)
+    want = np.asarray(oracle.matmul_q4(x.reshape(-1), wq, sc, ze, M, K, N, 32, K // 32), np.float32)
+    print(f"gemm fp32 wide tile M={M} y={y}", flush=True)
+    if y == "f16":
+        got = run_q4(hip, x, hip.F32, w, M, N, hip.F16)
+        ref_check(got, want.astype(np.float16).astype(np.float32), REF_TOL + 2.0 ** -10)
+    else:
+        xd = hip.DeviceBuffer.from_array(np.ascontiguousarray(x).reshape(-1))
+        yd = hip.DeviceBuffer(M * N * 2)
+        hip.q4_matmul(xd, hip.F32, w, yd, hip.BF16, M)
+        got = bf16_bits_to_f32(yd.read(np.uint16, M * N)).reshape(M, N)
+        ref_check(got, f32_to_bf16_rne(want), REF_TOL + 2.0 ** -7)
 
 
 @pytest.mark.parametrize("scales", ["tiny", "huge", "mixed"])

@@ -2,7 +2,8 @@
 byhip_q4_matmul through the C ABI.
 
 The shapes take the routes that use scratch: split-K on the skinny (M = 32) and large-tile
-(M = 256) GEMMs, the per-row shifts of fp32 activations, the exact GEMM's split-K, and the GEMV.
+(M = 256) GEMMs, the per-row shifts and fp16 planes of fp32 activations, the exact GEMM's
+split-K, and the GEMV.
 Each shape runs twice in a row on the static entry point, the second time with a smaller input, so
 the second call finds the first call's contents in the shared scratch. Bar: bit-identical to
 byhip_q4_matmul when both take the same split (they share the kernels), else the parity tiers.
@@ -26,7 +27,7 @@ def call(hip, fn, x, x_dtype, w, M, N, y_dtype):
     # (M first call, M second call, K, N, x dtype, y dtype, scales)
     (32, 16, 4096, 4096, "f16", "f16", "f16"),      # skinny GEMM, split-K
     (256, 130, 4096, 6144, "f16", "f16", "f16"),    # large tile, split-K
-    (64, 24, 1024, 512, "f32", "f32", "f16"),       # fp32 activations: per-row shifts
+    (64, 24, 1024, 512, "f32", "f32", "f16"),       # fp32 activations: shifts and fp16 planes
     (48, 12, 1024, 384, "f32", "f32", "tiny"),      # exact GEMM (weights outside fp16), split-K
     (4, 1, 4096, 2048, "f16", "f32", "f16"),        # GEMV (no scratch)
 ])
