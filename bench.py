@@ -206,6 +206,31 @@ def bench_c1(dev, synth, steps, warmup):
     return res
 
 
+def bench_c0(dev, synth, steps, warmup):
+    """Config 0's shape on the GPU at the reference's session dtype (fp32 activations and outputs,
+    M = 16, K = N = 4096), and the same weights at M = 512 (fp32 prefill): weights rotated past
+    the Infinity Cache as in c1."""
+    K, N = 4096, 4096
+    out = {}
+    copies = max(1, -(-ROTATE_BYTES // q4_bytes(1, K, N)))
+    g = synth.rng(0)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    ws = [dev.Q4Weights(wq, sc, ze, K, N, 32, K // 32) for _ in range(copies)]
+    for M in (16, 512):
+        x = dev.DeviceBuffer.from_array(synth.activations(g, M, K, np.float32).reshape(-1))
+        y = dev.DeviceBuffer(M * N * 4)
+        fn = lambda i, M=M, x=x, y=y: dev.q4_matmul(x, dev.F32, ws[i % copies], y, dev.F32, M)  # noqa: E731
+        gpu_s, _ = run_steps(fn, steps, warmup, settle_steps=copies)
+        per = gpu_s / steps
+        flops, b = 2 * M * K * N, q4_bytes(M, K, N) + M * K * 2 + M * N * 2  # fp32 x and y
+        out[f"M{M}"] = {"M": M, "K": K, "N": N, "us_per_step": per * 1e6, "TFLOPs": flops / per / 1e12,
+                        "GBps": b / per / 1e9}
+    out["weight_copies"] = copies
+    for w in ws:
+        w.close()
+    return out
+
+
 def bench_c2(dev, synth, steps, warmup):
     M, K, N = 512, 4096, 4096
     ws, x, y = q4_setup(dev, synth, 2, M, K, N, 1)
@@ -624,8 +649,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,up,rp",
-                    help="configurations to measure (c1 is the headline and always runs); c4t is c4 "
+    ap.add_argument("--configs", default="c0,c1,c2,c3,c4,up,rp",
+                    help="configurations to measure (c1 is the headline and always runs; c0 is config 0's shape at "
+                         "fp32 in and out, M = 16 and 512); c4t is c4 "
                          "with the batch timed again after byhip_q4_prepare tunes each projection")
     ap.add_argument("--cpu-seconds", type=float, default=0.8,
                     help="minimum seconds per CPU-baseline measurement (0: no CPU baseline)")
@@ -653,6 +679,8 @@ def main() -> int:
 
     c1 = bench_c1(dev, synth, args.steps, args.warmup)
     configs = {}
+    if "c0" in wanted:
+        configs["c0_session_fp32"] = bench_c0(dev, synth, args.steps, args.warmup)
     if "c2" in wanted:
         configs["c2_prefill_q4_gemm"] = bench_c2(dev, synth, args.steps, args.warmup)
     if "c3" in wanted:

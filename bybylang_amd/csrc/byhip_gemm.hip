@@ -318,15 +318,28 @@ __global__ __launch_bounds__(256) void row_range_shift(const float* __restrict__
 
 // fp32 activations for the wide tile: the row's shift t as row_range_shift finds it, and the
 // shifted row as two fp16 planes, hi = fp16(x 2^t) and lo = fp16(x 2^t - hi) (about 22 bits of x).
-// One block per row, K % 4 == 0, 16-byte aligned rows.
+// One block per row, K % 4 == 0, 16-byte aligned rows. The first kSplitHeld float4 of each thread
+// (K <= 8192) are loaded at once and stay in registers between the maximum and the split; the
+// rest of a longer row is read again.
+constexpr int kSplitHeld = 8;
 __global__ __launch_bounds__(256) void split_rows_f16(const float* __restrict__ x, int K, int* __restrict__ shifts,
                                                      _Float16* __restrict__ hi, _Float16* __restrict__ lo) {
     __shared__ float part[4];
     __shared__ int shift;
     const size_t row = (size_t)blockIdx.x * K;
     const float4* r = reinterpret_cast<const float4*>(x + row);
+    const int nq = K / 4;
+    float4 held[kSplitHeld];
     float mx = 0.0f;
-    for (int k = threadIdx.x; k < K / 4; k += 256) {
+#pragma unroll
+    for (int u = 0; u < kSplitHeld; ++u) {
+        const int k = (int)threadIdx.x + 256 * u;
+        held[u] = k < nq ? r[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitHeld; ++u)
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(held[u].x), fabsf(held[u].y))), fmaxf(fabsf(held[u].z), fabsf(held[u].w)));
+    for (int k = (int)threadIdx.x + 256 * kSplitHeld; k < nq; k += 256) {
         const float4 v = r[k];
         mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
     }
@@ -340,8 +353,7 @@ __global__ __launch_bounds__(256) void split_rows_f16(const float* __restrict__ 
     }
     __syncthreads();
     const int t = shift;
-    for (int k = threadIdx.x; k < K / 4; k += 256) {
-        const float4 v = r[k];
+    auto split = [&](int k, const float4 v) {
         const float s[4] = {__builtin_amdgcn_ldexpf(v.x, t), __builtin_amdgcn_ldexpf(v.y, t),
                             __builtin_amdgcn_ldexpf(v.z, t), __builtin_amdgcn_ldexpf(v.w, t)};
         uint16_t h[4], l[4];
@@ -353,7 +365,13 @@ __global__ __launch_bounds__(256) void split_rows_f16(const float* __restrict__ 
         }
         reinterpret_cast<uint2*>(hi + row)[k] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
         reinterpret_cast<uint2*>(lo + row)[k] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    };
+#pragma unroll
+    for (int u = 0; u < kSplitHeld; ++u) {
+        const int k = (int)threadIdx.x + 256 * u;
+        if (k < nq) split(k, held[u]);
     }
+    for (int k = (int)threadIdx.x + 256 * kSplitHeld; k < nq; k += 256) split(k, r[k]);
 }
 
 // Pipelined Q4 GEMM for the benchmark format: fp16 activations, fp16 scales, one integral zero,
