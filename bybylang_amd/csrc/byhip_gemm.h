@@ -72,6 +72,9 @@ void launch_splitk_sum(const GemmArgs& a, int splits);
 // weights are rounded once to fp16 (exact for F16 weights and for FP4-KM tables whose products
 // are halves; Q4 rounds (q - z) * s).
 void launch_gemm(BFormat fmt, const GemmArgs& a);
+// Whether launch_gemm(Q4Fast, a) takes a call with fp32 activations on the wide tile over two fp16
+// activation planes (the prefill copy's format conditions, and BYHIP_Q4_F32_WIDE not 0).
+bool q4_f32_wide_takes(const GemmArgs& a);
 
 // The exact route: each weight formed in fp32 exactly as the reference forms it (Q4
 // ((float)q - z) * s with any scales, zeros and group size; FP4-KM lut[nibble] * lut[16 + byte];

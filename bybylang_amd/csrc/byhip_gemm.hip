@@ -1873,6 +1873,8 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
     }
 }
 
+bool q4_f32_wide_takes(const GemmArgs& a) { return q4_wide_f32_ok(a) && env_int("BYHIP_Q4_F32_WIDE", 1) != 0; }
+
 void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.K % 32 != 0) fail("byhip: internal: GEMM needs K %% 32 == 0 (K=%d)", a.K);
     if (a.M <= 0 || a.N <= 0) return;
@@ -1880,7 +1882,7 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     switch (fmt) {
     case BFormat::Q4Fast:
         // fp32 activations: the wide tile on two fp16 planes where the scratch holds them
-        if (q4_wide_f32_ok(a) && env_int("BYHIP_Q4_F32_WIDE", 1) != 0 && launch_q4_wide_f32(a)) break;
+        if (q4_f32_wide_takes(a) && launch_q4_wide_f32(a)) break;
         if (q4_skinny_ok(a)) {
             launch_q4_skinny(a, 0, q4_small_wide(a));
             break;

@@ -396,7 +396,14 @@ bool q4_fast(const byhip_q4w* w) {
 
 // Routes y = x . W^T. Decode shapes (M <= 8) take the GEMV, whose arithmetic is exact (fp32 scales,
 // zeros and sums; fp32 activations kept to ~22 bits over their whole range), or the per-element
-// kernel when the GEMV does not take the shape. Larger M takes the fp16 MFMA kernels when the
+// kernel when the GEMV does not take the shape. Exception: fp32 activations on weights with the
+// prefill copy take the wide tile over two fp16 activation planes (the weights kept exactly, ~22
+// bits of x) from M = 3, and at M = 2 when one GEMV launch does not hold both rows. The GEMV's time
+// grows with its rows while the tile's barely moves (fp32, K x N = 4096 x 14336, M = 1 / 2 / 3 /
+// 4 / 8: GEMV 11.6 / 14.0 / 25.6 / 27.6 / 54.2 us, tile 15.6 / 15.8 / 15.9 / 16.1 / 16.6;
+// 14336 x 4096: GEMV 13.7 / 27.2 / 40.6 / 53.9 / 107.0, tile 18.6 / 19.2 / 19.3 / 19.5 / 20.7).
+// fp16 activations stay on the GEMV, which keeps the weights in fp32 where the fp16 tile rounds
+// them. Larger M takes the fp16 MFMA kernels when the
 // weights are fp16-safe (each (q - z) * s rounded once to fp16, byhip_q4w::f16_safe) and `exact`
 // is not asked for, else the exact fp32 GEMM. BYHIP_Q4_ROUTE forces a route: 1 GEMV, 2 GEMM (fp16
 // when safe, else exact), 3 per-element, 4 exact GEMM.
@@ -423,6 +430,10 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
     const bool gemv = aligned && q4_gemv_eligible(w, M, x_dtype);
     if (mode == 3) return launch_generic(x, x_dtype, w, y, y_dtype, M);
     if (mode == 4) return launch_gemm_exact(BFormat::Q4Generic, ga);
+    if (mode == 0 && M > 1 && M <= 8 && x_dtype == BYHIP_F32 && !exact && w->f16_safe && aligned &&
+        w->K % 32 == 0 && q4_fast(w) && q4_f32_wide_takes(ga) &&
+        !(M == 2 && gemv && gemv_rows_per_launch(w->K, M, x_dtype) >= 2))
+        return launch_gemm(BFormat::Q4Fast, ga);
     if (gemv && (mode == 1 || (mode == 0 && M <= 8))) return launch_q4_gemv(x, x_dtype, w, y, y_dtype, M);
     // Decode shapes the GEMV does not take stay on the exact per-element kernel.
     if (M <= 8 && mode != 2) return launch_generic(x, x_dtype, w, y, y_dtype, M);

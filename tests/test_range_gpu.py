@@ -4,7 +4,8 @@ The reference computes in fp32 for any decode table, any scales and any activati
 (cpu_vm.c:583-628, cpu_kernels_impl.inc:293-319); its own test draws its tables at random
 (t_fp4_tile_gemm.nim:35-44). The HIP routes must give the same numbers wherever the data lies:
   - fp32 activations spanning 1e-8 .. 1e6 on the decode GEMV (1, 2, 4 and 8 chunks per lane, so
-    K up to 14336), the fused GEMV, and the fp16 MFMA GEMM (per-row power-of-two shift, weight
+    K up to 14336), the fused GEMV, the fp16 MFMA GEMM and the wide tile over two fp16 activation
+    planes, which fp32 decode rows take from M = 3 (per-row power-of-two shift, weight
     remainders);
   - Q4 scales whose weights leave fp16's range (the exact fp32 GEMM);
   - FP4-KM tables whose products are not halves: every E8M0 byte 0..254, normal-distributed scale
@@ -165,14 +166,15 @@ def test_gemm_fp32_activations_split_k(hip, oracle, monkeypatch, M, splits):
 
 
 @pytest.mark.parametrize("splits", ["", "1", "3"])
-@pytest.mark.parametrize("M", [9, 16, 17, 40, 130, 512])
+@pytest.mark.parametrize("M", [2, 3, 5, 8, 9, 16, 17, 40, 130, 512])
 def test_gemm_fp32_activations_wide_tile(hip, oracle, monkeypatch, M, splits):
     """fp32 activations on weights with a prefill copy (fp16 scales, one zero): the 16- or 32-row
     wide tile on the activations' two fp16 planes (hi . w_hi + lo . w_hi + hi . w_lo), with the
     default K split, none, and 3 slices (rounded to whole rounds of the four K groups), ragged N
-    (320 = 2.5 column tiles) and M (17, 130); activations over 1e-8 .. 1e6 against the oracle at
-    the reference's fp32 tolerance, and the same rows with the wide tile switched off
-    (BYHIP_Q4_F32_WIDE=0, the generic GEMM) to the same bar."""
+    (320 = 2.5 column tiles) and M (decode rows 3 .. 8, which take the tile from M = 3, and 17,
+    130); activations over 1e-8 .. 1e6 against the oracle at the reference's fp32 tolerance, and
+    the same rows with the wide tile switched off (BYHIP_Q4_F32_WIDE=0: the GEMV up to M = 8, the
+    generic GEMM above) to the same bar."""
     g = synth.rng(7500 + M + 7 * len(splits))
     K, N = 2048, 320
     monkeypatch.setenv("BYHIP_Q4_SPLIT", splits)
@@ -186,8 +188,22 @@ def test_gemm_fp32_activations_wide_tile(hip, oracle, monkeypatch, M, splits):
     ref_check(run_q4(hip, x, hip.F32, w, M, N), want)
 
 
+@pytest.mark.parametrize("M", [2, 4, 8])
+def test_fp32_decode_rows_long_k(hip, oracle, M):
+    """fp32 decode rows at c4's down-projection K (14336, where one GEMV launch holds one row):
+    from M = 2 they take the wide tile; activations over 1e-8 .. 1e6 against the oracle at the
+    reference's fp32 tolerance."""
+    g = synth.rng(7550 + M)
+    K, N = 14336, 256
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    x = wide_x(g, M, K)
+    print(f"fp32 decode rows M={M} K={K}", flush=True)
+    ref_check(run_q4(hip, x, hip.F32, w, M, N), oracle.matmul_q4(x.reshape(-1), wq, sc, ze, M, K, N, 32, K // 32))
+
+
 @pytest.mark.parametrize("y", ["f16", "bf16"])
-@pytest.mark.parametrize("M", [12, 64])
+@pytest.mark.parametrize("M", [3, 12, 64])
 def test_gemm_fp32_activations_wide_tile_half_outputs(hip, oracle, M, y):
     """The fp32-activation wide tile writing fp16 and bf16 outputs: the oracle's fp32 result
     rounded to the output type, plus one step of that type (both roundings may land a step apart:

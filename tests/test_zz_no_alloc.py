@@ -30,6 +30,7 @@ def call(hip, fn, x, x_dtype, w, M, N, y_dtype):
     (64, 24, 1024, 512, "f32", "f32", "f16"),       # fp32 activations: shifts and fp16 planes
     (48, 12, 1024, 384, "f32", "f32", "tiny"),      # exact GEMM (weights outside fp16), split-K
     (4, 1, 4096, 2048, "f16", "f32", "f16"),        # GEMV (no scratch)
+    (6, 3, 4096, 2048, "f32", "f32", "f16"),        # fp32 decode rows on the wide tile
 ])
 def test_static_entry_matches_q4_matmul(hip, shape):
     M1, M2, K, N, xd, yd, scales = shape
