@@ -75,6 +75,10 @@ void launch_gemm(BFormat fmt, const GemmArgs& a);
 // Whether launch_gemm(Q4Fast, a) takes a call with fp32 activations on the wide tile over two fp16
 // activation planes (the prefill copy's format conditions, and BYHIP_Q4_F32_WIDE not 0).
 bool q4_f32_wide_takes(const GemmArgs& a);
+// Queues the 16- or 32-row wide tile on fp16 activations with each Q4 weight as two fp16 terms that
+// add up to it exactly (the weights' prefill copy, M <= 32); false, queueing nothing, when it does
+// not take the call.
+bool launch_q4_wide_exact_weights(const GemmArgs& a);
 
 // The exact route: each weight formed in fp32 exactly as the reference forms it (Q4
 // ((float)q - z) * s with any scales, zeros and group size; FP4-KM lut[nibble] * lut[16 + byte];

@@ -943,11 +943,18 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Operands of the wide tile: fp16 activations and weights rounded once to fp16 (kWideHalf); fp32
+// activations as a high and a low fp16 plane and the weights as two fp16 terms that add up to them
+// exactly (kWideF32); fp16 activations and the weights' two terms (kWideExactW).
+enum WideKind { kWideHalf = 1, kWideF32 = 2, kWideExactW = 3 };
+__host__ __device__ constexpr int wide_xplanes(int v) { return v == kWideF32 ? 2 : 1; }
+__host__ __device__ constexpr int wide_wplanes(int v) { return v == kWideHalf ? 1 : 2; }
+
 // Sizes for FM row fragments (BM = 16 FM rows: 64 for prefill, 32 or 16 for small M), D
-// activation buffers per group (loads D - 1 sub-steps ahead) and XS activation planes (1: fp16
-// activations; 2: fp32 activations as a high and a low fp16 plane).
-template <int FM, int D, int XS = 1>
+// activation buffers per group (loads D - 1 sub-steps ahead) and operand kind V.
+template <int FM, int D, int V = kWideHalf>
 struct WideShape {
+    static constexpr int XS = wide_xplanes(V);
     static constexpr int kBM = 16 * FM;
     static constexpr int kXBuf = XS * kBM * kWideSub * 2;     // one activation buffer (all planes)
     static constexpr int kLoads = XS * FM + 4 + 1;            // loads per wave and sub-step
@@ -977,12 +984,13 @@ struct WideStep {
     static constexpr bool guard = G;
 };
 
-template <int FM, int YT, int D = wide_depth(FM), int XS = 1>
+template <int FM, int YT, int D = wide_depth(FM), int V = kWideHalf>
 __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     static_assert(FM == 1 || FM == 2 || FM == 4, "q4_gemm_wide: 16, 32 or 64 rows");
-    static_assert(XS == 1 || (XS == 2 && FM <= 2), "q4_gemm_wide: two activation planes up to 32 rows");
+    constexpr int XS = wide_xplanes(V), WS = wide_wplanes(V);  // activation and weight planes
+    static_assert(V == kWideHalf || FM <= 2, "q4_gemm_wide: two operand planes up to 32 rows");
     constexpr int FN = 4;
-    using S = WideShape<FM, D, XS>;
+    using S = WideShape<FM, D, V>;
     constexpr int BM = S::kBM, kXBuf = S::kXBuf, kLoads = S::kLoads;
     static_assert(D >= 4 && S::kLds <= 160 * 1024 && (D - 2) * kLoads <= 63,
                   "q4_gemm_wide: the buffers must fit LDS and the loads in flight the wait counter");
@@ -1074,10 +1082,10 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
         for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
     // Weights of MFMA kk of a sub-step: (q - zero) * scale in fp16, exact in the subtraction. With
-    // two activation planes also the weight's low term: the product (q - zero) * scale has at most
+    // two weight planes also the weight's low term: the product (q - zero) * scale has at most
     // 15 significant bits, so hi = fp16 of it (one rounding) and lo = fma(q - zero, scale, -hi),
     // which an fp16 holds exactly, add up to it: plane [1] of bw.
-    auto dequant = [&](const WideW& r, int kk, h8 (&bw)[XS][FN]) __attribute__((always_inline)) {
+    auto dequant = [&](const WideW& r, int kk, h8 (&bw)[WS][FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const _Float16 sc = bits_h((uint16_t)(r.s[j >> 1] >> (16 * (j & 1))));
@@ -1090,12 +1098,12 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             const h2 w0 = q0 * ss, w1 = q1 * ss, w2 = q2 * ss, w3 = q3 * ss;
             const uint4 u = make_uint4(h2_bits(w0), h2_bits(w1), h2_bits(w2), h2_bits(w3));
             bw[0][j] = *reinterpret_cast<const h8*>(&u);
-            if constexpr (XS == 2) {
+            if constexpr (WS == 2) {
                 const uint4 l = make_uint4(h2_bits(__builtin_elementwise_fma(q0, ss, -w0)),
                                            h2_bits(__builtin_elementwise_fma(q1, ss, -w1)),
                                            h2_bits(__builtin_elementwise_fma(q2, ss, -w2)),
                                            h2_bits(__builtin_elementwise_fma(q3, ss, -w3)));
-                bw[XS - 1][j] = *reinterpret_cast<const h8*>(&l);
+                bw[WS - 1][j] = *reinterpret_cast<const h8*>(&l);
             }
         }
     };
@@ -1109,25 +1117,25 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
             for (int i = 0; i < FM; ++i) x[XS - 1][i] = *reinterpret_cast<const h8*>(src + 128 * BM + 2048 * i);
         }
     };
-    // x . w, and with two planes also x_lo . w_hi and x_hi . w_lo (x_lo . w_lo is below fp32's
-    // resolution of the sum).
-    auto mfmas = [&](const h8 (&x)[XS][FM], const h8 (&b)[XS][FN]) __attribute__((always_inline)) {
+    // x . w, with two activation planes also x_lo . w_hi, with two weight planes also x_hi . w_lo
+    // (x_lo . w_lo is below fp32's resolution of the sum).
+    auto mfmas = [&](const h8 (&x)[XS][FM], const h8 (&b)[WS][FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[0][i], b[0][j], acc[i][j], 0, 0, 0);
-                if constexpr (XS == 2) {
+                if constexpr (XS == 2)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[XS - 1][i], b[0][j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[0][i], b[XS - 1][j], acc[i][j], 0, 0, 0);
-                }
+                if constexpr (WS == 2)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[0][i], b[WS - 1][j], acc[i][j], 0, 0, 0);
             }
     };
 
     // Sub-steps 0 .. D - 2 are loaded here (activations, then weights), sub-step t + D - 1 in
     // sub-step t.
     WideW rs[D];
-    h8 ax0[XS][FM], ax1[XS][FM], bw0[XS][FN], bw1[XS][FN];
+    h8 ax0[XS][FM], ax1[XS][FM], bw0[WS][FN], bw1[WS][FN];
     static_for<D - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         load_x(k, k);
@@ -1143,8 +1151,8 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_wide(GemmArgs a) {
     // are dequantized), all indices mod D; t + D - 1's activations go to buffer k - 1, which every
     // wave's reads of t - 1 freed before the previous barrier. At the mid-step wait the loads of
     // t + 2 .. t + D - 1 may stay in flight, those that were issued.
-    constexpr int kMfmas = (XS == 2 ? 3 : 1) * FM * FN;                            // per K half
-    constexpr int kValuPerMfma = (FN * (XS == 2 ? 18 : 14) + kMfmas - 1) / kMfmas;  // a K half's dequantization
+    constexpr int kMfmas = (XS + WS - 1) * FM * FN;                                 // per K half
+    constexpr int kValuPerMfma = (FN * (WS == 2 ? 18 : 14) + kMfmas - 1) / kMfmas;  // a K half's dequantization
     auto step = [&](int t, auto kc, auto kind) __attribute__((always_inline)) {
         constexpr int k = decltype(kc)::value, k1 = (k + 1) % D, kp = (k + D - 1) % D;
         constexpr int kWait = decltype(kind)::wait;
@@ -1501,14 +1509,14 @@ void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
     BYHIP_LAUNCHED("q4_gemm_skinny");
 }
 
-template <int FM, int XS = 1>
+template <int FM, int V = kWideHalf>
 void launch_q4_wide_shape(const GemmArgs& a, int splits) {
     const dim3 grid((a.N + kWideBN - 1) / kWideBN, (a.M + 16 * FM - 1) / (16 * FM), splits);
     constexpr int D = wide_depth(FM);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F32, D, XS>), grid, dim3(512), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F16, D, XS>), grid, dim3(512), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_BF16, D, XS>), grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F32, D, V>), grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F16, D, V>), grid, dim3(512), 0, stream(), a); break;
+    default: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_BF16, D, V>), grid, dim3(512), 0, stream(), a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_wide");
 }
@@ -1707,11 +1715,28 @@ bool q4_wide_f32_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 128) * a.row_bytes < kLim && (uint64_t)(a.N + 128) * a.gpr * 2 < kLim;
 }
 
+// The 16- or 32-row wide tile with operand kind V (two weight planes) on a.x (and a.x_lo): K split
+// as for the fp16 tile (whole rounds of the four K groups), then splitk_sum.
+template <int V>
+void launch_q4_wide_planes(GemmArgs a, int split_choice) {
+    const int bm = a.M <= 16 ? 16 : 32;
+    const long tiles = (long)((a.N + kWideBN - 1) / kWideBN) * ((a.M + bm - 1) / bm);
+    const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
+    int splits = choose_split(a, tiles, a.K / kWideSub, 1, forced > 0 ? forced : wide_splits(a, tiles), 1);
+    if (a.part) {
+        a.split_steps = (a.split_steps + 3) / 4 * 4;
+        splits = (a.K / kWideSub + a.split_steps - 1) / a.split_steps;
+    }
+    if (splits == 1) a.part = nullptr;
+    if (bm == 16) launch_q4_wide_shape<1, V>(a, splits);
+    else launch_q4_wide_shape<2, V>(a, splits);
+    if (a.part) launch_splitk_sum(a, splits);
+}
+
 // The wide tile on fp32 activations: per row a power-of-two shift onto fp16's range and the shifted
 // row as two fp16 planes (split_rows_f16, into the scratch), then the 16- or 32-row tile with three
 // MFMAs per product (hi . w_hi + lo . w_hi + hi . w_lo), every fp32 weight and about 22 bits of
-// each activation kept; K split as for the fp16 tile. False, queueing nothing, when the planes do
-// not fit the scratch.
+// each activation kept. False, queueing nothing, when the planes do not fit the scratch.
 bool launch_q4_wide_f32(const GemmArgs& a0, int split_choice = 0) {
     GemmArgs a = a0;
     uint8_t* const work = static_cast<uint8_t*>(a.work ? a.work : workspace());
@@ -1730,19 +1755,7 @@ bool launch_q4_wide_f32(const GemmArgs& a0, int split_choice = 0) {
     a.row_shift = shifts;
     a.work = work + shift_bytes + 2 * plane;
     a.work_bytes = work_bytes - shift_bytes - 2 * plane;
-    const int bm = a.M <= 16 ? 16 : 32;
-    const long tiles = (long)((a.N + kWideBN - 1) / kWideBN) * ((a.M + bm - 1) / bm);
-    const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
-    int splits = choose_split(a, tiles, a.K / kWideSub, 1, forced > 0 ? forced : wide_splits(a, tiles), 1);
-    if (a.part) {
-        // whole rounds of the four groups
-        a.split_steps = (a.split_steps + 3) / 4 * 4;
-        splits = (a.K / kWideSub + a.split_steps - 1) / a.split_steps;
-    }
-    if (splits == 1) a.part = nullptr;
-    if (bm == 16) launch_q4_wide_shape<1, 2>(a, splits);
-    else launch_q4_wide_shape<2, 2>(a, splits);
-    if (a.part) launch_splitk_sum(a, splits);
+    launch_q4_wide_planes<kWideF32>(a, split_choice);
     return true;
 }
 
@@ -1874,6 +1887,12 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
 }
 
 bool q4_f32_wide_takes(const GemmArgs& a) { return q4_wide_f32_ok(a) && env_int("BYHIP_Q4_F32_WIDE", 1) != 0; }
+
+bool launch_q4_wide_exact_weights(const GemmArgs& a) {
+    if (a.M > 32 || !q4_wide_ok(a)) return false;
+    launch_q4_wide_planes<kWideExactW>(a, 0);
+    return true;
+}
 
 void launch_gemm(BFormat fmt, const GemmArgs& a) {
     if (a.K % 32 != 0) fail("byhip: internal: GEMM needs K %% 32 == 0 (K=%d)", a.K);

@@ -402,10 +402,14 @@ bool q4_fast(const byhip_q4w* w) {
 // grows with its rows while the tile's barely moves (fp32, K x N = 4096 x 14336, M = 1 / 2 / 3 /
 // 4 / 8: GEMV 11.6 / 14.0 / 25.6 / 27.6 / 54.2 us, tile 15.6 / 15.8 / 15.9 / 16.1 / 16.6;
 // 14336 x 4096: GEMV 13.7 / 27.2 / 40.6 / 53.9 / 107.0, tile 18.6 / 19.2 / 19.3 / 19.5 / 20.7).
-// fp16 activations stay on the GEMV, which keeps the weights in fp32 where the fp16 tile rounds
-// them. Larger M takes the fp16 MFMA kernels when the
-// weights are fp16-safe (each (q - z) * s rounded once to fp16, byhip_q4w::f16_safe) and `exact`
-// is not asked for, else the exact fp32 GEMM. BYHIP_Q4_ROUTE forces a route: 1 GEMV, 2 GEMM (fp16
+// fp16 activations take the wide tile with each weight as two fp16 terms that add up to it (the
+// weights exact, as in the GEMV) past 4 rows, or past the rows one GEMV launch holds (fp16,
+// M = 2 / 4 / 5 / 8: 4096 x 14336 GEMV 9.9 / 13.8 / 21.1 / 27.2 us, tile 12.6 / 12.6 / 12.7 /
+// 12.7; 14336 x 4096, one row per GEMV launch, GEMV 15.9 / 31.0 / 38.5 / 60.8, tile 12.5 / 12.8 /
+// 12.9 / 13.0; 4096 x 6144 GEMV 6.3 / 9.0 / 13.7 / 17.9, tile 9.6 / 9.6 / 9.7 / 9.9).
+// BYHIP_Q4_DECODE_TILE=0 keeps them on the GEMV, 1 puts them on the tile from M = 2.
+// Larger M takes the fp16 MFMA kernels when the weights are fp16-safe (each (q - z) * s rounded
+// once to fp16, byhip_q4w::f16_safe) and `exact` is not asked for, else the exact fp32 GEMM. BYHIP_Q4_ROUTE forces a route: 1 GEMV, 2 GEMM (fp16
 // when safe, else exact), 3 per-element, 4 exact GEMM.
 void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, bool exact,
                     void* work, size_t work_bytes) {
@@ -434,6 +438,14 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
         w->K % 32 == 0 && q4_fast(w) && q4_f32_wide_takes(ga) &&
         !(M == 2 && gemv && gemv_rows_per_launch(w->K, M, x_dtype) >= 2))
         return launch_gemm(BFormat::Q4Fast, ga);
+    {
+        const int dt = env_int("BYHIP_Q4_DECODE_TILE", -1);
+        if (mode == 0 && M > 1 && M <= 8 && x_dtype == BYHIP_F16 && !exact && w->f16_safe && aligned &&
+            q4_fast(w) &&
+            (dt == 1 || (dt < 0 && (M > 4 || !gemv || gemv_rows_per_launch(w->K, M, x_dtype) < M))) &&
+            launch_q4_wide_exact_weights(ga))
+            return;
+    }
     if (gemv && (mode == 1 || (mode == 0 && M <= 8))) return launch_q4_gemv(x, x_dtype, w, y, y_dtype, M);
     // Decode shapes the GEMV does not take stay on the exact per-element kernel.
     if (M <= 8 && mode != 2) return launch_generic(x, x_dtype, w, y, y_dtype, M);

@@ -202,6 +202,26 @@ def test_fp32_decode_rows_long_k(hip, oracle, M):
     ref_check(run_q4(hip, x, hip.F32, w, M, N), oracle.matmul_q4(x.reshape(-1), wq, sc, ze, M, K, N, 32, K // 32))
 
 
+@pytest.mark.parametrize("tile", ["", "1", "0"])
+@pytest.mark.parametrize("K,N", [(4096, 320), (14336, 256)])
+@pytest.mark.parametrize("M", [2, 3, 5, 8])
+def test_fp16_decode_rows_exact_weights(hip, oracle, monkeypatch, M, K, N, tile):
+    """fp16 decode rows on the wide tile with each weight as two fp16 terms that add up to it
+    (past 4 rows, or past what one GEMV launch holds: one row at K = 14336), forced onto it
+    (BYHIP_Q4_DECODE_TILE=1) and off it (0: the GEMV); the weights stay exact, so the bar is the
+    reference's fp32 tolerance against the oracle on the fp16 activations."""
+    g = synth.rng(7560 + M + K)
+    monkeypatch.setenv("BYHIP_Q4_DECODE_TILE", tile)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    w = hip.Q4Weights(wq, sc, ze, K, N, 32, K // 32)
+    xh = synth.activations(g, M, K, np.float16)
+    want = oracle.matmul_q4(xh.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    print(f"fp16 decode rows M={M} K={K} tile={tile or 'default'}", flush=True)
+    ref_check(run_q4(hip, xh, hip.F16, w, M, N), want)
+    got16 = run_q4(hip, xh, hip.F16, w, M, N, hip.F16)
+    ref_check(got16, np.asarray(want, np.float32).astype(np.float16).astype(np.float32), REF_TOL + 2.0 ** -10)
+
+
 @pytest.mark.parametrize("y", ["f16", "bf16"])
 @pytest.mark.parametrize("M", [3, 12, 64])
 def test_gemm_fp32_activations_wide_tile_half_outputs(hip, oracle, M, y):
