@@ -81,15 +81,23 @@ __device__ __forceinline__ void load_bytes(rsrc_t r, uint32_t off, uint32_t* w) 
 template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK, int YT>
 __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     constexpr int XS = XF32 ? 2 : 1;
-    // A single fp32 row of more than 4 chunks per lane does not fit the register tile: its
-    // activations are then read from LDS where each weight row uses them.
-    constexpr bool XLDS = M * CPL * XS > 8;
+    // A single fp32 row reads its activations from LDS where each weight row uses them: past 4
+    // chunks per lane they do not fit the register tile, and below it holding them took the
+    // registers of 3 waves per SIMD (K = 4096: 107 VGPRs, 4 waves per SIMD, against 7 reading
+    // LDS; 11.6 -> 9.7 us at N = 14336, 5.3 -> 4.8 at N = 4096, together with XHALF).
+    constexpr bool XLDS = M * CPL * XS > 8 || (XF32 && M == 1);
     static_assert(!XLDS || M == 1, "the launcher slices rows so that only one-row launches read x from LDS");
     constexpr int R = gemv_rows(M, CPL);
     constexpr uint32_t XB = XF32 ? 4 : 2;  // bytes per activation
     constexpr int XW = XF32 ? 8 : 4;       // 16-byte activation loads per 32-value chunk
     // activation chunks a thread stages: M * G <= M * 64 * CPL chunks over 256 threads (at most 512)
     constexpr int XC = (M * CPL + 3) / 4 < 2 ? (M * CPL + 3) / 4 : 2;
+    // fp32 activations with at most 256 half chunks: each thread stages half a chunk (16 values),
+    // the pair of lanes sharing the chunk's maximum and sum, so that the staging holds 16 values
+    // per thread instead of 32 (with x read from LDS, the staging was the register peak at M = 1,
+    // K <= 4096)
+    constexpr bool XHALF = XF32 && M * CPL <= 2;
+    constexpr int XWL = XHALF ? XW / 2 : XW;  // 16-byte activation loads a thread issues per chunk
     constexpr uint32_t SB = SF16 ? 2u : 4u;
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
 
@@ -125,15 +133,17 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
         gsel[c] = BLK ? (uint32_t)cc : (uint32_t)(a.group_chunks ? cc / a.group_chunks : 0);
     }
 
-    // 1. the activations this thread stages (chunks tid and tid + 256 of the M x G chunks)
-    uint4 xraw[XC][XW];
+    // 1. the activations this thread stages (chunks tid and tid + 256 of the M x G chunks; with
+    // XHALF half hf = tid & 1 of chunk tid / 2)
+    uint4 xraw[XC][XWL];
+    const int hf = XHALF ? (tid & 1) : 0;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
-        const int idx = tid + 256 * i;
+        const int idx = XHALF ? tid >> 1 : tid + 256 * i;
         const int m = idx / G, ci = idx - m * G;
-        const uint32_t base = idx < M * G ? (uint32_t)m * K * XB + (uint32_t)ci * 32u * XB : kOutOfRange;
+        const uint32_t base = idx < M * G ? (uint32_t)m * K * XB + (uint32_t)ci * 32u * XB + 64u * (uint32_t)hf : kOutOfRange;
 #pragma unroll
-        for (int t = 0; t < XW; ++t) xraw[i][t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
+        for (int t = 0; t < XWL; ++t) xraw[i][t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
     }
 
     // 2. scales and zeros of the wave's R rows
@@ -185,8 +195,54 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);  // every load is out before the first wait
 
     // 4. stage the activations: fp16 pairs matching the nibble pairs, and the chunk sums
+    if constexpr (XHALF) {
+        // values 16 hf .. 16 hf + 15 of chunk idx: pieces 2 hf and 2 hf + 1 (both lanes of a pair
+        // take the branch together, so each reads its partner's maximum and sum)
+        const int idx = tid >> 1;
+        if (idx < M * G) {
+            float v[16];
 #pragma unroll
-    for (int i = 0; i < XC; ++i) {
+            for (int t = 0; t < 4; ++t) {
+                v[4 * t] = __builtin_bit_cast(float, xraw[0][t].x);
+                v[4 * t + 1] = __builtin_bit_cast(float, xraw[0][t].y);
+                v[4 * t + 2] = __builtin_bit_cast(float, xraw[0][t].z);
+                v[4 * t + 3] = __builtin_bit_cast(float, xraw[0][t].w);
+            }
+            float mx = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) mx = fmaxf(mx, fabsf(v[t]));
+            mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
+            const int sh = fp16_range_shift(mx);
+            float s = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                v[t] = __builtin_amdgcn_ldexpf(v[t], sh);
+                s += v[t];
+            }
+            s += __shfl_xor(s, 1, kWave);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t p[4], lo[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float u = v[8 * j + q], w = v[8 * j + q + 4];
+                    const _Float16 hu = (_Float16)u, hw = (_Float16)w;
+                    const _Float16 lu = (_Float16)(u - (float)hu), lw = (_Float16)(w - (float)hw);
+                    p[q] = (uint32_t)h_bits(hu) | ((uint32_t)h_bits(hw) << 16);
+                    lo[q] = (uint32_t)h_bits(lu) | ((uint32_t)h_bits(lw) << 16);
+                }
+                const int t = 2 * hf + j;
+                reinterpret_cast<uint4*>(xh)[idx + t * M * G] = make_uint4(p[0], p[1], p[2], p[3]);
+                reinterpret_cast<uint4*>(xl)[idx + t * M * G] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            }
+            if (hf == 0) {
+                sums[2 * idx] = __builtin_amdgcn_ldexpf(1.0f, -sh);  // the back-scale rides in the bias slot
+                sums[2 * idx + 1] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (XHALF ? 0 : XC); ++i) {
         const int idx = tid + 256 * i;
         if (idx < M * G) {
             uint32_t p[16], lo[16];
