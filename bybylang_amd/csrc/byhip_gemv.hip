@@ -543,19 +543,25 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
 
     // 1. the first input chunk this thread stages (chunk tid; chunk tid + 256 follows after the
     // weight loads are out) and its norm weights
+    // Up to 2 chunks per lane (G <= 128) each thread stages half a chunk, values 16 hf .. 16 hf + 15
+    // of chunk tid / 2, and the two lanes of a chunk exchange its maximum and sum: the staging
+    // registers (the kernel's peak, beside the weights in flight) hold 16 values instead of 32.
+    constexpr bool HALF = CPL <= 2;
+    constexpr int XW = HALF ? 4 : 8;  // 16-byte loads per staged piece
+    const int hf = HALF ? (tid & 1) : 0;
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)K * 4u);
     const rsrc_t gr = make_rsrc(a.gamma ? a.gamma : a.x, a.gamma ? (uint32_t)K * 4u : 0u);
     auto load_chunk = [&](int idx, uint4* xraw, uint4* graw) {
-        const uint32_t base = idx < G ? (uint32_t)idx * 128u : kOutOfRange;
+        const uint32_t base = idx < G ? (uint32_t)idx * 128u + 64u * (uint32_t)hf : kOutOfRange;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xraw[t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
+        for (int t = 0; t < XW; ++t) xraw[t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
         if (a.gamma) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) graw[t] = buf_load16(gr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
+            for (int t = 0; t < XW; ++t) graw[t] = buf_load16(gr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
         }
     };
-    uint4 xraw[8], graw[8];
-    load_chunk(tid, xraw, graw);
+    uint4 xraw[XW], graw[XW];
+    load_chunk(HALF ? tid >> 1 : tid, xraw, graw);
 
     // 2. scales and zeros, 3. weight rows of the wave's batch (per matrix), all before the first wait
     uint32_t sraw[NM][R][CPL], zraw[NM][R][CPL];
@@ -603,9 +609,10 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     float ssq = 0.0f;
     auto stage_chunk = [&](int idx, const uint4* xraw, const uint4* graw) {
         if (idx >= G) return;
-        float v[32];
+        constexpr int NV = 4 * XW;  // values this thread holds
+        float v[NV];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < XW; ++t) {
             v[4 * t] = __builtin_bit_cast(float, xraw[t].x);
             v[4 * t + 1] = __builtin_bit_cast(float, xraw[t].y);
             v[4 * t + 2] = __builtin_bit_cast(float, xraw[t].z);
@@ -613,7 +620,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
         }
         if (a.gamma) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
+            for (int t = 0; t < XW; ++t) {
                 const float gm[4] = {__builtin_bit_cast(float, graw[t].x), __builtin_bit_cast(float, graw[t].y),
                                      __builtin_bit_cast(float, graw[t].z), __builtin_bit_cast(float, graw[t].w)};
 #pragma unroll
@@ -626,13 +633,14 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
         // the chunk onto fp16's range (x * 2^sh), as in q4_gemv
         float mx = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 32; ++t) mx = fmaxf(mx, fabsf(v[t]));
+        for (int t = 0; t < NV; ++t) mx = fmaxf(mx, fabsf(v[t]));
+        if constexpr (HALF) mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
         const int sh = fp16_range_shift(mx);
 #pragma unroll
-        for (int t = 0; t < 32; ++t) v[t] = __builtin_amdgcn_ldexpf(v[t], sh);
-        uint32_t p[16], lo[16];
+        for (int t = 0; t < NV; ++t) v[t] = __builtin_amdgcn_ldexpf(v[t], sh);
+        uint32_t p[NV / 2], lo[NV / 2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NV / 8; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float u = v[8 * j + q], w = v[8 * j + q + 4];
@@ -643,19 +651,23 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
             }
         float s = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 32; ++t) s += v[t];
+        for (int t = 0; t < NV; ++t) s += v[t];
+        if constexpr (HALF) s += __shfl_xor(s, 1, kWave);
         uint4* dh = reinterpret_cast<uint4*>(xh) + idx;
         uint4* dl = reinterpret_cast<uint4*>(xl) + idx;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            dh[t * G] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
-            dl[t * G] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
+        for (int t = 0; t < NV / 8; ++t) {
+            const int piece = (NV / 8) * hf + t;  // 0 .. 3
+            dh[piece * G] = make_uint4(p[4 * t], p[4 * t + 1], p[4 * t + 2], p[4 * t + 3]);
+            dl[piece * G] = make_uint4(lo[4 * t], lo[4 * t + 1], lo[4 * t + 2], lo[4 * t + 3]);
         }
-        sums[idx] = s;
-        facs[idx] = __builtin_amdgcn_ldexpf(1.0f, -sh);
+        if (hf == 0) {
+            sums[idx] = s;
+            facs[idx] = __builtin_amdgcn_ldexpf(1.0f, -sh);
+        }
     };
-    stage_chunk(tid, xraw, graw);
-    if (G > 256) {  // K > 8192: a second chunk per thread (G <= 512)
+    stage_chunk(HALF ? tid >> 1 : tid, xraw, graw);
+    if (!HALF && G > 256) {  // K > 8192: a second chunk per thread (G <= 512)
         load_chunk(tid + 256, xraw, graw);
         stage_chunk(tid + 256, xraw, graw);
     }
