@@ -700,40 +700,41 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const int idx = (int)(coff[c] >> 4);
-            uint32_t xp[16], xq[16];
             const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
             const uint4* sl = reinterpret_cast<const uint4*>(xl) + idx;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint4 u = sh[t * G], w = sl[t * G];
-                xp[4 * t] = u.x; xp[4 * t + 1] = u.y; xp[4 * t + 2] = u.z; xp[4 * t + 3] = u.w;
-                xq[4 * t] = w.x; xq[4 * t + 1] = w.y; xq[4 * t + 2] = w.z; xq[4 * t + 3] = w.w;
-            }
             const float sxc = sums[idx], fac = facs[idx];
+            // piece by piece (4 input pairs and their low terms at a time), every row's dot product
+            // in the same order as one row at a time: the input registers are 8, not 32
+            float p[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t dw[4] = {wv[j][r][c].x, wv[j][r][c].y, wv[j][r][c].z, wv[j][r][c].w};
-                float p = 0.0f;
+            for (int r = 0; r < R; ++r) p[r] = 0.0f;
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint32_t d8 = dw[w] >> 8;
-                    const h2 q0 = bits_h2((dw[w] & 0x000F000Fu) | mag_lo) - bias_lo;
-                    const h2 q1 = bits_h2((dw[w] & 0x00F000F0u) | mag_hi) - bias_hi;
+            for (int w = 0; w < 4; ++w) {
+                const uint4 u = sh[w * G], l = sl[w * G];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t d = w == 0 ? wv[j][r][c].x : w == 1 ? wv[j][r][c].y : w == 2 ? wv[j][r][c].z : wv[j][r][c].w;
+                    const uint32_t d8 = d >> 8;
+                    const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo) - bias_lo;
+                    const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi) - bias_hi;
                     const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo) - bias_lo;
                     const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi) - bias_hi;
-                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 0]), q0, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 0]), q0, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 1]), q1, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 1]), q1, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 2]), q2, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 2]), q2, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xp[4 * w + 3]), q3, p, false);
-                    p = __builtin_amdgcn_fdot2(bits_h2(xq[4 * w + 3]), q3, p, false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.x), q0, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.x), q0, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.y), q1, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.y), q1, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.z), q2, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.z), q2, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.w), q3, p[r], false);
+                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.w), q3, p[r], false);
                 }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
                 float sc = SF16 ? (float)bits_h((uint16_t)sraw[j][r][c]) : __builtin_bit_cast(float, sraw[j][r][c]);
                 sc = cv[c] ? sc : 0.0f;
                 const float z = ZU ? fm.zero_value : __builtin_bit_cast(float, zraw[j][r][c]);
-                acc[r] = fmaf(sc * fac, p - z * sxc, acc[r]);
+                acc[r] = fmaf(sc * fac, p[r] - z * sxc, acc[r]);
             }
         }
 #pragma unroll
