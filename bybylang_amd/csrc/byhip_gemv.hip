@@ -667,21 +667,28 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
         }
     };
     stage_chunk(HALF ? tid >> 1 : tid, xraw, graw);
-    if (!HALF && G > 256) {  // K > 8192: a second chunk per thread (G <= 512)
-        load_chunk(tid + 256, xraw, graw);
-        stage_chunk(tid + 256, xraw, graw);
-    }
-    ssq_part[tid] = ssq;
+    // K > 8192 (8 chunks per lane): the second input chunk of each thread (chunks 256 ..) is
+    // loaded after the weight loads, so its wait is the wait for all of them; the wave first runs
+    // its chunks below 256 (c < 4), staged before the first barrier, while its later weights
+    // stream in, then stages the second chunk and runs c >= 4 after a second barrier. Each row's
+    // sum keeps the chunk order.
+    constexpr bool TWO = CPL == 8;
+    if constexpr (TWO) load_chunk(tid + 256, xraw, graw);
+    else ssq_part[tid] = ssq;
     __syncthreads();
-    if (!live) return;
-
+    if constexpr (!TWO) {
+        if (!live) return;
+    }
     // norm factor: the 256 partials in a fixed order (lane l adds l, l + 64, l + 128, l + 192)
     float inv = 1.0f;
-    if (a.gamma) {
-        const float t = (ssq_part[lane] + ssq_part[lane + 64]) + (ssq_part[lane + 128] + ssq_part[lane + 192]);
-        const float total = wave_sum_lane63(t);
-        inv = 1.0f / sqrtf(total / (float)K + a.eps);  // meaningful on lane 63, which stores
-    }
+    auto norm_factor = [&]() {
+        if (a.gamma) {
+            const float t = (ssq_part[lane] + ssq_part[lane + 64]) + (ssq_part[lane + 128] + ssq_part[lane + 192]);
+            const float total = wave_sum_lane63(t);
+            inv = 1.0f / sqrtf(total / (float)K + a.eps);  // meaningful on lane 63, which stores
+        }
+    };
+    if constexpr (!TWO) norm_factor();
 
     uint32_t mag_lo, mag_hi;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
@@ -690,56 +697,73 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
 
     // 5. chunks in load order, each chunk's input pairs read from LDS once for all the wave's rows;
     // then the wave sums (lane 63) and the epilogue on lane 63
-    float dots[NM][R];
+    float acc[NM][R];
 #pragma unroll
-    for (int j = 0; j < NM; ++j) {
-        const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
-        float acc[R];
+    for (int j = 0; j < NM; ++j)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        for (int r = 0; r < R; ++r) acc[j][r] = 0.0f;
+    auto run_chunks = [&](auto c_lo, auto c_hi) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int idx = (int)(coff[c] >> 4);
-            const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
-            const uint4* sl = reinterpret_cast<const uint4*>(xl) + idx;
-            const float sxc = sums[idx], fac = facs[idx];
-            // piece by piece (4 input pairs and their low terms at a time), every row's dot product
-            // in the same order as one row at a time: the input registers are 8, not 32
-            float p[R];
+        for (int j = 0; j < NM; ++j) {
+            const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
 #pragma unroll
-            for (int r = 0; r < R; ++r) p[r] = 0.0f;
+            for (int c = decltype(c_lo)::value; c < decltype(c_hi)::value; ++c) {
+                const int idx = (int)(coff[c] >> 4);
+                const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
+                const uint4* sl = reinterpret_cast<const uint4*>(xl) + idx;
+                const float sxc = sums[idx], fac = facs[idx];
+                // piece by piece (4 input pairs and their low terms at a time), every row's dot product
+                // in the same order as one row at a time: the input registers are 8, not 32
+                float p[R];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint4 u = sh[w * G], l = sl[w * G];
+                for (int r = 0; r < R; ++r) p[r] = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint4 u = sh[w * G], l = sl[w * G];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const uint32_t d = w == 0 ? wv[j][r][c].x : w == 1 ? wv[j][r][c].y : w == 2 ? wv[j][r][c].z : wv[j][r][c].w;
+                        const uint32_t d8 = d >> 8;
+                        const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo) - bias_lo;
+                        const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi) - bias_hi;
+                        const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo) - bias_lo;
+                        const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi) - bias_hi;
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(u.x), q0, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(l.x), q0, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(u.y), q1, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(l.y), q1, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(u.z), q2, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(l.z), q2, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(u.w), q3, p[r], false);
+                        p[r] = __builtin_amdgcn_fdot2(bits_h2(l.w), q3, p[r], false);
+                    }
+                }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const uint32_t d = w == 0 ? wv[j][r][c].x : w == 1 ? wv[j][r][c].y : w == 2 ? wv[j][r][c].z : wv[j][r][c].w;
-                    const uint32_t d8 = d >> 8;
-                    const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo) - bias_lo;
-                    const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi) - bias_hi;
-                    const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo) - bias_lo;
-                    const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi) - bias_hi;
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.x), q0, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.x), q0, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.y), q1, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.y), q1, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.z), q2, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.z), q2, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(u.w), q3, p[r], false);
-                    p[r] = __builtin_amdgcn_fdot2(bits_h2(l.w), q3, p[r], false);
+                    float sc = SF16 ? (float)bits_h((uint16_t)sraw[j][r][c]) : __builtin_bit_cast(float, sraw[j][r][c]);
+                    sc = cv[c] ? sc : 0.0f;
+                    const float z = ZU ? fm.zero_value : __builtin_bit_cast(float, zraw[j][r][c]);
+                    acc[j][r] = fmaf(sc * fac, p[r] - z * sxc, acc[j][r]);
                 }
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float sc = SF16 ? (float)bits_h((uint16_t)sraw[j][r][c]) : __builtin_bit_cast(float, sraw[j][r][c]);
-                sc = cv[c] ? sc : 0.0f;
-                const float z = ZU ? fm.zero_value : __builtin_bit_cast(float, zraw[j][r][c]);
-                acc[r] = fmaf(sc * fac, p[r] - z * sxc, acc[r]);
-            }
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r) dots[j][r] = wave_sum_lane63(acc[r]);
+    };
+    if constexpr (TWO) {
+        if (live) run_chunks(std::integral_constant<int, 0>{}, std::integral_constant<int, 4>{});
+        stage_chunk(tid + 256, xraw, graw);
+        ssq_part[tid] = ssq;
+        __syncthreads();
+        if (!live) return;
+        norm_factor();
+        run_chunks(std::integral_constant<int, 4>{}, std::integral_constant<int, CPL>{});
+    } else {
+        run_chunks(std::integral_constant<int, 0>{}, std::integral_constant<int, CPL>{});
     }
+    float dots[NM][R];
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+#pragma unroll
+        for (int r = 0; r < R; ++r) dots[j][r] = wave_sum_lane63(acc[j][r]);
     if (lane == 63) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
