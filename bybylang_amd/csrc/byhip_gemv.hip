@@ -500,14 +500,15 @@ struct FusedArgs {
     FusedMat m[3];
 };
 
-// Rows per wave and matrix: 4, or 2 when a row takes 8 chunks per lane (the weights a wave keeps
-// in flight) and for gate and up up to K = 4096 (106 VGPRs against 129: 4 waves per SIMD instead
-// of 3; gate+up over 2 x 14336 rows 17.5 -> 16.7 us).
-constexpr int fused_rows(int cpl, int mode) { return cpl >= 8 || (mode == 1 && cpl <= 2) ? 2 : 4; }
+// Rows per wave and matrix: 2 when a row takes 8 chunks per lane (the weights a wave keeps in
+// flight) and up to K = 4096, else 4. At K = 4096 two rows gave more waves with shorter tails:
+// gate+up (2 x 14336 rows) 106 VGPRs against 129, 4 waves per SIMD instead of 3, 17.5 -> 16.7 us;
+// QKV 6.35 -> 6.0 us, O 4.72 -> 4.65.
+constexpr int fused_rows(int cpl) { return cpl >= 8 || cpl <= 2 ? 2 : 4; }
 
 template <int CPL, bool SF16, bool ZU, int MODE>
 __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
-    constexpr int R = fused_rows(CPL, MODE);
+    constexpr int R = fused_rows(CPL);
     constexpr int NM = MODE == 1 ? 2 : 1;  // matrices a wave reads
     constexpr uint32_t SB = SF16 ? 2u : 4u;
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
@@ -886,7 +887,7 @@ void launch_q4_gemv_fused(int mode, const float* x, const byhip_q4w* const* ws, 
                           const float* res, const float* gamma, float eps) {
     FusedArgs a{};
     const int cpl = gemv_cpl(ws[0]->K);
-    const int rows = fused_rows(cpl, mode);
+    const int rows = fused_rows(cpl);
     a.x = x; a.res = res; a.gamma = gamma; a.eps = eps;
     a.K = ws[0]->K; a.row_bytes = (int)ws[0]->row_bytes; a.nmats = n_ws;
     int batches = 0;
