@@ -21,10 +21,10 @@ which bybylang_amd.profile_summary writes from two rocprofv3 --pmc runs of this 
 library's copy kernel moving a known number of bytes in the same run; null when that file is
 absent.
 
-cpu_baseline: the reference's own CPU path for this op (nimf_cpu_matmul_q4,
-backends/cpu/cpu_kernels_impl.inc:293-319, compiled from its sources into oracle/_ref), single
-threaded as the reference runs, on full config-1 passes; when that library is absent, the C
-restatement in oracle/ ("port"). cpu_baselines: the same path on every configuration (the CPU VM's
+cpu_baseline: the reference's CPU path for this op (nimf_cpu_matmul_q4,
+backends/cpu/cpu_kernels_impl.inc:293-319) through its C restatement in oracle/ (kind "port", pinned
+bit-exact to the reference's own C on the CPU tests), single threaded as the reference runs, on full
+config-1 passes. cpu_baselines: the same path on every configuration (the CPU VM's
 OP_TILE_GEMM for the FP4 one), on one core and on all the host's cores (at most 16, the box's
 share), splitting rows or columns over threads with bit-identical per-output loops; configs whose
 full run would take minutes time a stated row subset and scale linearly in M.
@@ -100,6 +100,9 @@ MARKS_IN_RECORDING = os.environ.get("BENCH_MARKS", "1") != "0"
 # region, so the per-step figures are upper bounds; the kernel durations the profiler reports
 # are the kernels' own.
 EAGER = False
+# --graph: recordings are HIP graphs. By default they keep their launches and replay them directly
+# (byhip_session_set_direct_replay), so that a kernel-trace profiler sees exactly the timed launches.
+GRAPH = False
 
 
 def run_steps_eager(fn, steps, warmup, settle_steps=8):
@@ -204,6 +207,46 @@ def bench_c1(dev, synth, steps, warmup):
     for w in ws:
         w.close()
     return res
+
+
+def bench_long_k(dev, synth, steps, warmup):
+    """Decode at long rows (the GEMV in K slices): a 70B-class down projection, M = 1, K = 28,672,
+    N = 8,192, fp16 x and y, weights rotated past the Infinity Cache as in c1; and the fused
+    silu(gate) * up GEMV over two such matrices' shape (K = 28,672, N = 2 x 4,096, fp32 input
+    with the norm)."""
+    out = {}
+    M, K, N = 1, 28672, 8192
+    nbytes = q4_bytes(M, K, N)
+    copies = max(1, -(-ROTATE_BYTES // nbytes))
+    ws, x, y = q4_setup(dev, synth, 5, M, K, N, copies)
+    fn = lambda i: dev.q4_matmul(x, dev.F16, ws[i % copies], y, dev.F16, M)  # noqa: E731
+    gpu_s, _ = run_steps(fn, steps, warmup, settle_steps=copies)
+    per = gpu_s / steps
+    out["gemv_M1_K28672_N8192"] = {"us": per * 1e6, "GBps": nbytes / per / 1e9, "bytes": nbytes}
+    for w in ws:
+        w.close()
+    Kf, Nf = 28672, 4096
+    fb = fused_bytes(1, Kf, [Nf, Nf], True, False)
+    copies = max(1, -(-ROTATE_BYTES // fb))
+    g = synth.rng(6)
+    mats = []
+    for _ in range(2):
+        wq, sc, ze, _ = synth.q4_weights(g, Nf, Kf)
+        mats.append([dev.Q4Weights(wq, sc, ze, Kf, Nf, 32, Kf // 32) for _ in range(copies)])
+    a = dev.DeviceBuffer.from_array(g.standard_normal(Kf).astype(np.float32))
+    gamma = dev.DeviceBuffer.from_array((1.0 + 0.1 * g.standard_normal(Kf)).astype(np.float32))
+    outs = [dev.DeviceBuffer(Nf * 4) for _ in range(2)]
+
+    def call(i):
+        assert dev.q4_matmul_fused(1, a, [m[i % copies] for m in mats], outs, None, gamma, 1e-5) == 0
+
+    gpu_s, _ = run_steps(call, steps, warmup, settle_steps=copies)
+    per = gpu_s / steps
+    out["fused_gate_up_norm_K28672_N4096x2"] = {"us": per * 1e6, "GBps": fb / per / 1e9, "bytes": fb}
+    for m in mats:
+        for w in m:
+            w.close()
+    return out
 
 
 def bench_c0(dev, synth, steps, warmup):
@@ -429,49 +472,33 @@ def bench_c4_fused(dev, synth, steps, warmup):
 
 
 class CpuPath:
-    """The reference's CPU path for this op, timed on the host: its own C compiled from its sources
-    into oracle/_ref (kind "reference": nimf_cpu_matmul_q4 for Q4, the CPU VM's OP_TILE_GEMM for
-    FP4-KM), else the C restatement in oracle/ ("port"). The reference runs single-threaded; the
-    all-core figures split rows (or, at M = 1, columns) over threads, each thread running the
-    same per-output loops, so the outputs are bit-identical to one thread's."""
+    """The reference's CPU path for this op, timed on the host through its C restatement in
+    oracle/ (kind "port"): orc_matmul_q4 (nimf_cpu_matmul_q4, cpu_kernels_impl.inc:293-319) for
+    Q4 and orc_tile_gemm (the CPU VM's OP_TILE_GEMM, cpu_vm.c:583-628) for FP4-KM, the same loops
+    in the same order, bit-exact to the reference's own C on the CPU tests. The reference runs
+    single-threaded; the all-core figures split rows (or, at M = 1, columns) over threads, each
+    thread running the same per-output loops, so the outputs are bit-identical to one thread's."""
 
     def __init__(self):
-        ref = os.path.join(ROOT, "oracle", "_ref", "libbybyref.so")
         port = os.path.join(ROOT, "oracle", "liboracle.so")
-        if os.path.exists(ref):
-            self.lib, self.kind = C.CDLL(ref), "reference"
-            self.lib.refshim_matmul_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 5
-            self.lib.refshim_vm_run_slots.argtypes = ([C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
-                                                      C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
-                                                      C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_int])
-        elif os.path.exists(port):
-            self.lib, self.kind = C.CDLL(port), "port"
-            self.lib.orc_matmul_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 7
-            self.lib.orc_tile_gemm.argtypes = ([C.c_uint32] * 4 + [C.c_uint64] * 2 +
-                                               [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p,
-                                                C.c_int64, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32,
-                                                C.c_char_p, C.c_int])
-        else:
-            raise FileNotFoundError("no CPU path built (oracle/_ref or oracle/liboracle.so)")
+        if not os.path.exists(port):
+            raise FileNotFoundError("no CPU path built (oracle/liboracle.so)")
+        self.lib, self.kind = C.CDLL(port), "port"
+        self.lib.orc_matmul_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 7
+        self.lib.orc_tile_gemm.argtypes = ([C.c_uint32] * 4 + [C.c_uint64] * 2 +
+                                           [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p,
+                                            C.c_int64, C.c_void_p, C.c_int64, C.c_uint32, C.c_uint32,
+                                            C.c_char_p, C.c_int])
 
     def q4(self, a, wq, sc, ze, c, M, K, N):
         """Q4 group 32 on host pointers (a [M, K] fp32, rows of wq, fp32 scales / zeros, c [M, N])."""
-        if self.kind == "reference":
-            self.lib.refshim_matmul_q4(a, wq, sc, ze, c, M, K, N, 32, K // 32)
-        else:
-            self.lib.orc_matmul_q4(a, wq, sc, ze, c, M, K, N, 32, K // 32, 0, M)
+        self.lib.orc_matmul_q4(a, wq, sc, ze, c, M, K, N, 32, K // 32, 0, M)
 
     def fp4(self, x, blob, blob_len, table, out, M, K, N):
-        """The FP4-KM tile GEMM (the c3 format) on M rows: the CPU VM running OP_TILE_GEMM."""
-        if self.kind == "reference":
-            code = np.array([0xB0, M, K, N, N * (K // 2), 0, 0x01], dtype=np.uint32)
-            err = C.create_string_buffer(256)
-            rc = self.lib.refshim_vm_run_slots(code.ctypes.data, code.size, out, M * N, blob, blob_len,
-                                               table, 272, x, M * K, 128, 64, 128, err, 256)
-        else:
-            err = C.create_string_buffer(256)
-            rc = self.lib.orc_tile_gemm(0, M, K, N, N * (K // 2), 0, blob, blob_len, table, 272, x, M * K,
-                                        out, M * N, 0, M, err, 256)
+        """The FP4-KM tile GEMM (the c3 format) on M rows: the CPU VM's OP_TILE_GEMM."""
+        err = C.create_string_buffer(256)
+        rc = self.lib.orc_tile_gemm(0, M, K, N, N * (K // 2), 0, blob, blob_len, table, 272, x, M * K,
+                                    out, M * N, 0, M, err, 256)
         assert rc == 0, err.value
 
 
@@ -589,7 +616,8 @@ def cpu_baseline(baselines):
     c1 = baselines["c1"]
     return {"value": c1["GBps_1core"], "unit": "GB/s", "cores": 1, "kind": baselines["kind"],
             "sample": f"full config-1 passes (M=1 K=4096 N=14336, fp32 x), {c1['s_1core'] * 1e3:.1f} ms each, "
-                      f"nimf_cpu_matmul_q4 single thread on {baselines['cpu_model']}; on {baselines['threads']} "
+                      f"orc_matmul_q4 (C restatement of nimf_cpu_matmul_q4, bit-exact to the reference build) single "
+                      f"thread on {baselines['cpu_model']}; on {baselines['threads']} "
                       f"threads {c1['GBps_all']:.2f} GB/s"}
 
 
@@ -649,7 +677,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--configs", default="c0,c1,c2,c3,c4,up,rp",
+    ap.add_argument("--configs", default="c0,c1,c2,c3,c4,lk,up,rp",
                     help="configurations to measure (c1 is the headline and always runs; c0 is config 0's shape at "
                          "fp32 in and out, M = 16 and 512); c4t is c4 "
                          "with the batch timed again after byhip_q4_prepare tunes each projection")
@@ -658,10 +686,14 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run the copy kernel on MIB MiB (calibration for counter runs)")
     ap.add_argument("--eager", action="store_true",
-                    help="launch every step directly instead of replaying recordings (profiler runs)")
+                    help="launch every step directly from Python instead of replaying recordings")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the recordings as HIP graphs (the default replays their kept launches "
+                         "directly; graph replays are never run under a profiler)")
     args = ap.parse_args()
-    global EAGER
+    global EAGER, GRAPH
     EAGER = args.eager
+    GRAPH = args.graph
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.stderr.write("bench.py measures one GPU only: this build has no multi-GPU path "
                          "(collectives are out of scope); run with --gpus 1\n")
@@ -673,6 +705,8 @@ def main() -> int:
     from bybylang_amd import device as dev
     from bybylang_amd import synth
     dev.init(0)
+    from bybylang_amd import _abi
+    _abi.check(_abi.load().byhip_session_set_direct_replay(0 if GRAPH else 1), "replay mode")
     info = dev.device_info()
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
     probe = copy_probe(args.copy_probe) if args.copy_probe > 0 else 0
@@ -687,6 +721,8 @@ def main() -> int:
         configs["c3_mxfp4_gemm"] = bench_c3(dev, synth, args.steps, args.warmup)
     if "c4" in wanted or "c4t" in wanted:
         configs["c4_layer_batch"] = bench_c4(dev, synth, args.steps, args.warmup, tuned="c4t" in wanted)
+    if "lk" in wanted:
+        configs["long_k_decode"] = bench_long_k(dev, synth, args.steps, args.warmup)
     if "up" in wanted:
         configs["resident_upload_mapped"] = bench_upload_mapped(synth)
     if "rp" in wanted:
@@ -714,8 +750,9 @@ def main() -> int:
                    "timing": ("eager launches (profiler run): 200 ms settle, `warmup` steps, then `steps` "
                               "timed launches between two realtime-counter marks, host launch gaps included"
                               if EAGER else
-                              "one recording (HIP graph): rotation lead-in, `warmup` steps, then `steps` timed "
-                              "launches between two realtime-counter marks; 200 ms settle before"),
+                              "one recording (%s): rotation lead-in, `warmup` steps, then `steps` timed "
+                              "launches between two realtime-counter marks; 200 ms settle before"
+                              % ("HIP graph" if GRAPH else "kept launches replayed directly on the stream")),
                    "device": info.get("name", ""), "arch": info.get("arch_name", ""),
                    "compute_units": info.get("compute_units")},
         "roofline": {"bound": "hbm", "achieved": round(c1["GBps"], 2), "peak": HBM_PEAK_GBS,

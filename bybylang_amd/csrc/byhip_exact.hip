@@ -189,9 +189,9 @@ __global__ __launch_bounds__(256) void gemm_f32_exact(GemmArgs a) {
 template <BFormat F, bool XF32>
 void launch_exact_bm(const GemmArgs& a, int bm, dim3 grid) {
     switch (bm) {
-    case 16: hipLaunchKernelGGL((gemm_f32_exact<F, XF32, 16>), grid, dim3(256), 0, stream(), a); break;
-    case 32: hipLaunchKernelGGL((gemm_f32_exact<F, XF32, 32>), grid, dim3(256), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((gemm_f32_exact<F, XF32, 64>), grid, dim3(256), 0, stream(), a); break;
+    case 16: launch("gemm_f32_exact", (gemm_f32_exact<F, XF32, 16>), grid, dim3(256), 0, a); break;
+    case 32: launch("gemm_f32_exact", (gemm_f32_exact<F, XF32, 32>), grid, dim3(256), 0, a); break;
+    default: launch("gemm_f32_exact", (gemm_f32_exact<F, XF32, 64>), grid, dim3(256), 0, a); break;
     }
     BYHIP_LAUNCHED("gemm_f32_exact");
 }

@@ -413,8 +413,14 @@ int byhip_debug_unpack_fp4km(const uint8_t* blob, size_t scale_base, const float
         const size_t total = (size_t)N * K;
         uint8_t* dc = static_cast<uint8_t*>(device_alloc(total));
         float* dw = static_cast<float*>(device_alloc(total * 4));
-        hipLaunchKernelGGL(fp4km_unpack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream(), blob,
-                           scale_base, lut + lut_base, K, N, dc, dw);
+        try {
+            launch("fp4km_unpack", fp4km_unpack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, blob,
+                               scale_base, lut + lut_base, K, N, dc, dw);
+        } catch (...) {
+            device_free(dc);
+            device_free(dw);
+            throw;
+        }
         hipError_t e = hipGetLastError();
         if (e == hipSuccess) e = hipStreamSynchronize(stream());
         if (e == hipSuccess) e = hipMemcpy(codes, dc, total, hipMemcpyDeviceToHost);

@@ -5,6 +5,9 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <utility>
+
+#include "byhip_kernels.h"
 
 namespace byhip {
 
@@ -56,6 +59,67 @@ struct GemmArgs {
     // x_lo the low one (x * 2^t = hi + lo, t per row in row_shift).
     const void* x_lo = nullptr;
 };
+
+// Whether 8-output chunks may leave as 16-byte stores: every row of y (or of the split-K
+// partials) starts 16-byte aligned.
+template <int YT>
+__device__ __forceinline__ bool out8_vector_ok(const GemmArgs& a, const float* part) {
+    constexpr int es = YT == BYHIP_F32 ? 4 : 2;
+    return part ? a.N % 4 == 0 : ((uintptr_t)a.y % 16 == 0 && (size_t)a.N * es % 16 == 0);
+}
+
+// Outputs v[0..7] of row m, columns n .. n + 7, to y (or to the split-K partials `part`): one
+// 16-byte store (fp16 / bf16) or two (fp32) when `vec` and all 8 columns exist, else one store per
+// column inside N.
+template <int YT>
+__device__ __forceinline__ void store_out8(const GemmArgs& a, float* part, bool vec, int m, int n, const float (&v)[8]) {
+    if (vec && n + 8 <= a.N) {
+        if (part || YT == BYHIP_F32) {
+            float* dst = part ? part + (size_t)m * a.N + n : static_cast<float*>(a.y) + (size_t)m * a.N + n;
+            reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+            reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (YT == BYHIP_F16)
+                    w[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e]) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]) << 16);
+                else
+                    w[e] = f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]);
+            }
+            *reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.y) + ((size_t)m * a.N + n) * 2) =
+                make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        if (n + e >= a.N) break;
+        if (part) part[(size_t)m * a.N + n + e] = v[e];
+        else store_y<YT>(a.y, (size_t)m * a.N + n + e, v[e]);
+    }
+}
+
+// LDS slot swizzle of the activation slices (rows of 128 bytes, eight 16-byte chunks): chunk k of
+// row r sits at slot k ^ x_swizzle(r), row bits 2, 1, 3 giving slot bits 0, 1, 2. With the fragment
+// reads (lane (c, g) reads chunk 2 g + kk of row 16 i + c, 16 bytes) this layout measured free of
+// LDS bank conflicts on the MI355X (a standalone probe of that read pattern with the hardware's
+// conflict counter): 2.3-2.5 ns per wave-wide read per CU, as fast as contiguous reads, against
+// 3.7-4.0 ns and 4 conflict cycles per read with the slot k ^ (r / 2 % 8) used before.
+__host__ __device__ constexpr int x_swizzle(int r) {
+    return ((r >> 2) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+}
+
+// Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // Floats between consecutive split-K partials (16-byte aligned).
 __host__ __device__ __forceinline__ size_t splitk_stride(int M, int N) { return ((size_t)M * N + 3) & ~(size_t)3; }

@@ -654,47 +654,6 @@ struct SkinnyLds {
     static constexpr int kBytes = kX > kRed ? kX : kRed;
 };
 
-// Whether 8-output chunks may leave as 16-byte stores: every row of y (or of the split-K
-// partials) starts 16-byte aligned.
-template <int YT>
-__device__ __forceinline__ bool out8_vector_ok(const GemmArgs& a, const float* part) {
-    constexpr int es = YT == BYHIP_F32 ? 4 : 2;
-    return part ? a.N % 4 == 0 : ((uintptr_t)a.y % 16 == 0 && (size_t)a.N * es % 16 == 0);
-}
-
-// Outputs v[0..7] of row m, columns n .. n + 7, to y (or to the split-K partials `part`): one
-// 16-byte store (fp16 / bf16) or two (fp32) when `vec` and all 8 columns exist, else one store per
-// column inside N.
-template <int YT>
-__device__ __forceinline__ void store_out8(const GemmArgs& a, float* part, bool vec, int m, int n, const float (&v)[8]) {
-    if (vec && n + 8 <= a.N) {
-        if (part || YT == BYHIP_F32) {
-            float* dst = part ? part + (size_t)m * a.N + n : static_cast<float*>(a.y) + (size_t)m * a.N + n;
-            reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
-            reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
-        } else {
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if constexpr (YT == BYHIP_F16)
-                    w[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e]) |
-                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]) << 16);
-                else
-                    w[e] = f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1]);
-            }
-            *reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.y) + ((size_t)m * a.N + n) * 2) =
-                make_uint4(w[0], w[1], w[2], w[3]);
-        }
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        if (n + e >= a.N) break;
-        if (part) part[(size_t)m * a.N + n + e] = v[e];
-        else store_y<YT>(a.y, (size_t)m * a.N + n + e, v[e]);
-    }
-}
-
 template <int BM, int FN, int YT>
 __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
     static_assert(FN <= 4 && BM <= 32, "q4_gemm_skinny: 16 or 32 rows, at most 4 column fragments");
@@ -922,26 +881,6 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_skinny(GemmArgs a) {
 constexpr int kWideBN = 128;
 constexpr int kWideSub = 64;                         // K values per sub-step
 constexpr int kWidePitch = out_pitch(kWideBN / 16);  // floats per row of a staged partial tile
-
-// LDS slot swizzle of the activation slices (rows of 128 bytes, eight 16-byte chunks): chunk k of
-// row r sits at slot k ^ x_swizzle(r), row bits 2, 1, 3 giving slot bits 0, 1, 2. With the fragment
-// reads (lane (c, g) reads chunk 2 g + kk of row 16 i + c, 16 bytes) this layout measured free of
-// LDS bank conflicts on the MI355X (a standalone probe of that read pattern with the hardware's
-// conflict counter): 2.3-2.5 ns per wave-wide read per CU, as fast as contiguous reads, against
-// 3.7-4.0 ns and 4 conflict cycles per read with the slot k ^ (r / 2 % 8) used before.
-__host__ __device__ constexpr int x_swizzle(int r) {
-    return ((r >> 2) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
-}
-
-// Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // Operands of the wide tile: fp16 activations and weights rounded once to fp16 (kWideHalf); fp32
 // activations as a high and a low fp16 plane and the weights as two fp16 terms that add up to them
@@ -1502,9 +1441,9 @@ template <int BM, int FN>
 void launch_q4_skinny_shape(const GemmArgs& a, int splits) {
     const dim3 grid((a.N + 16 * FN - 1) / (16 * FN), (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_skinny<BM, FN, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_skinny<BM, FN, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((q4_gemm_skinny<BM, FN, BYHIP_BF16>), grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F32: launch("q4_gemm_skinny", (q4_gemm_skinny<BM, FN, BYHIP_F32>), grid, dim3(256), 0, a); break;
+    case BYHIP_F16: launch("q4_gemm_skinny", (q4_gemm_skinny<BM, FN, BYHIP_F16>), grid, dim3(256), 0, a); break;
+    default: launch("q4_gemm_skinny", (q4_gemm_skinny<BM, FN, BYHIP_BF16>), grid, dim3(256), 0, a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_skinny");
 }
@@ -1514,9 +1453,9 @@ void launch_q4_wide_shape(const GemmArgs& a, int splits) {
     const dim3 grid((a.N + kWideBN - 1) / kWideBN, (a.M + 16 * FM - 1) / (16 * FM), splits);
     constexpr int D = wide_depth(FM);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F32, D, V>), grid, dim3(512), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_F16, D, V>), grid, dim3(512), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((q4_gemm_wide<FM, BYHIP_BF16, D, V>), grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F32: launch("q4_gemm_wide", (q4_gemm_wide<FM, BYHIP_F32, D, V>), grid, dim3(512), 0, a); break;
+    case BYHIP_F16: launch("q4_gemm_wide", (q4_gemm_wide<FM, BYHIP_F16, D, V>), grid, dim3(512), 0, a); break;
+    default: launch("q4_gemm_wide", (q4_gemm_wide<FM, BYHIP_BF16, D, V>), grid, dim3(512), 0, a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_wide");
 }
@@ -1536,9 +1475,9 @@ template <int BM, int BN>
 void launch_q4_pipe_shape(const GemmArgs& a, int splits) {
     const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_F32>), grid, dim3(256), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_F16>), grid, dim3(256), 0, stream(), a); break;
-    default: hipLaunchKernelGGL((q4_gemm_pipe<BM, BN, BYHIP_BF16>), grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F32: launch("q4_gemm_pipe", (q4_gemm_pipe<BM, BN, BYHIP_F32>), grid, dim3(256), 0, a); break;
+    case BYHIP_F16: launch("q4_gemm_pipe", (q4_gemm_pipe<BM, BN, BYHIP_F16>), grid, dim3(256), 0, a); break;
+    default: launch("q4_gemm_pipe", (q4_gemm_pipe<BM, BN, BYHIP_BF16>), grid, dim3(256), 0, a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_pipe");
 }
@@ -1566,17 +1505,17 @@ void launch_splitk_sum(const GemmArgs& a, int splits) {
     if (grid.x < (unsigned)compute_units()) {  // fp32 route M = 9 .. 32: 0.2-0.4 us faster
         const dim3 g1((unsigned)(((size_t)a.M * a.N + 255) / 256));
         switch (a.y_dtype) {
-        case BYHIP_F32: hipLaunchKernelGGL(splitk_sum1<BYHIP_F32>, g1, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
-        case BYHIP_F16: hipLaunchKernelGGL(splitk_sum1<BYHIP_F16>, g1, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
-        default: hipLaunchKernelGGL(splitk_sum1<BYHIP_BF16>, g1, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
+        case BYHIP_F32: launch("splitk_sum1", splitk_sum1<BYHIP_F32>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
+        case BYHIP_F16: launch("splitk_sum1", splitk_sum1<BYHIP_F16>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
+        default: launch("splitk_sum1", splitk_sum1<BYHIP_BF16>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
         }
         BYHIP_LAUNCHED("splitk_sum1");
         return;
     }
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL(splitk_sum<BYHIP_F32>, grid, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
-    case BYHIP_F16: hipLaunchKernelGGL(splitk_sum<BYHIP_F16>, grid, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
-    default: hipLaunchKernelGGL(splitk_sum<BYHIP_BF16>, grid, dim3(256), 0, stream(), a.part, splits, a.M, a.N, a.y); break;
+    case BYHIP_F32: launch("splitk_sum", splitk_sum<BYHIP_F32>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
+    case BYHIP_F16: launch("splitk_sum", splitk_sum<BYHIP_F16>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
+    default: launch("splitk_sum", splitk_sum<BYHIP_BF16>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
     }
     BYHIP_LAUNCHED("splitk_sum");
 }
@@ -1638,9 +1577,9 @@ void launch_q4_big(const GemmArgs& a0, int split_choice = 0) {
     const int splits = choose_split(a, tiles, a.K / kWideSub, 8, forced);
     const dim3 grid((a.N + kTallBN - 1) / kTallBN, (a.M + kTallBM - 1) / kTallBM, splits);
     switch (a.y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL(q4_gemm_tall<BYHIP_F32>, grid, dim3(512), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL(q4_gemm_tall<BYHIP_F16>, grid, dim3(512), 0, stream(), a); break;
-    default: hipLaunchKernelGGL(q4_gemm_tall<BYHIP_BF16>, grid, dim3(512), 0, stream(), a); break;
+    case BYHIP_F32: launch("q4_gemm_tall", q4_gemm_tall<BYHIP_F32>, grid, dim3(512), 0, a); break;
+    case BYHIP_F16: launch("q4_gemm_tall", q4_gemm_tall<BYHIP_F16>, grid, dim3(512), 0, a); break;
+    default: launch("q4_gemm_tall", q4_gemm_tall<BYHIP_BF16>, grid, dim3(512), 0, a); break;
     }
     BYHIP_LAUNCHED("q4_gemm_tall");
     if (a.part) launch_splitk_sum(a, splits);
@@ -1747,7 +1686,7 @@ bool launch_q4_wide_f32(const GemmArgs& a0, int split_choice = 0) {
     int* const shifts = reinterpret_cast<int*>(work);
     _Float16* const hi = reinterpret_cast<_Float16*>(work + shift_bytes);
     _Float16* const lo = reinterpret_cast<_Float16*>(work + shift_bytes + plane);
-    hipLaunchKernelGGL(split_rows_f16, dim3((unsigned)a.M), dim3(256), 0, stream(), static_cast<const float*>(a.x), a.K,
+    launch("split_rows_f16", split_rows_f16, dim3((unsigned)a.M), dim3(256), 0, static_cast<const float*>(a.x), a.K,
                        shifts, hi, lo);
     BYHIP_LAUNCHED("split_rows_f16");
     a.x = hi;
@@ -1812,13 +1751,13 @@ void launch_fx(const GemmArgs& a0) {
     const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
     switch (a.y_dtype) {
     case BYHIP_F32:
-        hipLaunchKernelGGL((gemm_f16_mfma<F, XF32, BYHIP_F32>), grid, dim3(256), 0, stream(), a);
+        launch("gemm_f16_mfma", (gemm_f16_mfma<F, XF32, BYHIP_F32>), grid, dim3(256), 0, a);
         break;
     case BYHIP_F16:
-        hipLaunchKernelGGL((gemm_f16_mfma<F, XF32, BYHIP_F16>), grid, dim3(256), 0, stream(), a);
+        launch("gemm_f16_mfma", (gemm_f16_mfma<F, XF32, BYHIP_F16>), grid, dim3(256), 0, a);
         break;
     default:
-        hipLaunchKernelGGL((gemm_f16_mfma<F, XF32, BYHIP_BF16>), grid, dim3(256), 0, stream(), a);
+        launch("gemm_f16_mfma", (gemm_f16_mfma<F, XF32, BYHIP_BF16>), grid, dim3(256), 0, a);
         break;
     }
     BYHIP_LAUNCHED("gemm_f16_mfma");
@@ -1837,7 +1776,7 @@ void launch_f(const GemmArgs& a0) {
     const size_t work_bytes = a.work ? a.work_bytes : kWorkspaceBytes;
     if ((size_t)a.M * sizeof(int) > work_bytes) fail("byhip: M=%d rows of fp32 activations exceed the scratch", a.M);
     int* shifts = static_cast<int*>(work);
-    hipLaunchKernelGGL(row_range_shift, dim3((unsigned)a.M), dim3(256), 0, stream(), static_cast<const float*>(a.x), a.K,
+    launch("row_range_shift", row_range_shift, dim3((unsigned)a.M), dim3(256), 0, static_cast<const float*>(a.x), a.K,
                        shifts);
     BYHIP_LAUNCHED("row_range_shift");
     a.row_shift = shifts;

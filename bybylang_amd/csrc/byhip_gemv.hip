@@ -30,6 +30,7 @@
 // (an absolute error below 2^-39 of that largest value). Non-finite inputs give non-finite outputs.
 #include <algorithm>
 
+#include "byhip_gemm.h"
 #include "byhip_gemv.h"
 #include "byhip_internal.h"
 #include "byhip_kernels.h"
@@ -57,6 +58,11 @@ struct GemvArgs {
     float zero_value;
     void* y;
     int K, N, group_chunks, gpr, row_bytes, n_pad;
+    // K slices (blockIdx.y): slice z takes chunks z * slice_chunks .. of the Gt 32-value chunks of
+    // a row and, when there are several, writes fp32 partial sums to y + z * ystride (split-K);
+    // ldx is the activation row stride in elements.
+    int Gt, slice_chunks, ldx;
+    size_t ystride;
 };
 
 template <int NB>
@@ -102,7 +108,10 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int K = a.K, N = a.N, G = K >> 5;
+    const int N = a.N, Gt = a.Gt;
+    // this block's K slice: chunks c0 .. c0 + G - 1 of a row
+    const int c0 = blockIdx.y * a.slice_chunks;
+    const int G = min(a.slice_chunks, Gt - c0);
     const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * R);
     const bool rows_live = n0 < N;  // uniform in the wave; every wave takes part in the barrier
 
@@ -116,21 +125,25 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     float* sums = reinterpret_cast<float*>(xl + (XS == 2 ? M * G * 16 : 0));  // [M][G]{bias, sum}
 
     const rsrc_t wr = make_rsrc(a.wq, (uint32_t)N * (uint32_t)a.row_bytes);
-    const rsrc_t xr = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * XB);
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)M * (uint32_t)a.ldx * XB);
     const uint32_t srows = BLK ? (uint32_t)a.n_pad : (uint32_t)N;
-    const rsrc_t sr = make_rsrc(a.scales, srows * (uint32_t)(BLK ? G : a.gpr) * SB);
-    const rsrc_t zr = make_rsrc(ZU ? a.scales : a.zeros, ZU ? 0u : srows * (uint32_t)(BLK ? G : a.gpr) * 4u);
+    const rsrc_t sr = make_rsrc(a.scales, srows * (uint32_t)(BLK ? Gt : a.gpr) * SB);
+    const rsrc_t zr = make_rsrc(ZU ? a.scales : a.zeros, ZU ? 0u : srows * (uint32_t)(BLK ? Gt : a.gpr) * 4u);
 
-    // This lane's chunks (chunks past K are clamped onto the last one and their scale is zeroed).
+    // This lane's chunks of the slice (chunks past its end are clamped onto its last one and their
+    // scale is zeroed): lch is the chunk within the slice (the staging index), coff its byte offset
+    // in the weight row.
     uint32_t coff[CPL], gsel[CPL];
+    int lch[CPL];
     bool cv[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int ci = lane + kWave * c;
         cv[c] = ci < G;
         const int cc = min(ci, G - 1);
-        coff[c] = (uint32_t)cc * 16u;
-        gsel[c] = BLK ? (uint32_t)cc : (uint32_t)(a.group_chunks ? cc / a.group_chunks : 0);
+        lch[c] = cc;
+        coff[c] = (uint32_t)(c0 + cc) * 16u;
+        gsel[c] = BLK ? (uint32_t)(c0 + cc) : (uint32_t)(a.group_chunks ? (c0 + cc) / a.group_chunks : 0);
     }
 
     // 1. the activations this thread stages (chunks tid and tid + 256 of the M x G chunks; with
@@ -141,7 +154,8 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     for (int i = 0; i < XC; ++i) {
         const int idx = XHALF ? tid >> 1 : tid + 256 * i;
         const int m = idx / G, ci = idx - m * G;
-        const uint32_t base = idx < M * G ? (uint32_t)m * K * XB + (uint32_t)ci * 32u * XB + 64u * (uint32_t)hf : kOutOfRange;
+        const uint32_t base = idx < M * G ? (uint32_t)m * (uint32_t)a.ldx * XB + (uint32_t)(c0 + ci) * 32u * XB + 64u * (uint32_t)hf
+                                          : kOutOfRange;
 #pragma unroll
         for (int t = 0; t < XWL; ++t) xraw[i][t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
     }
@@ -154,7 +168,7 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     for (int c = 0; c < CPL; ++c) {
         if constexpr (BLK) {
             // rows n0 .. n0+R-1 of chunk c sit together: [(n0/8) * G + chunk] * 8 + n0 % 8
-            const uint32_t e = ((uint32_t)(nb >> 3) * (uint32_t)G + gsel[c]) * 8u + (uint32_t)(nb & 7);
+            const uint32_t e = ((uint32_t)(nb >> 3) * (uint32_t)Gt + gsel[c]) * 8u + (uint32_t)(nb & 7);
             uint32_t sw[R * SB / 4];
             load_bytes<R * SB>(sr, e * SB, sw);
 #pragma unroll
@@ -327,7 +341,7 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     uint32_t xq[XS == 2 ? XM : 1][XS == 2 ? XCP : 1][16];
     float bias[M][CPL], sx[M][CPL];
     auto read_x = [&](int m, int c, uint32_t* hp, uint32_t* lp) {
-        const int idx = m * G + (int)(coff[c] >> 4);
+        const int idx = m * G + lch[c];
         const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -347,7 +361,7 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const int idx = m * G + (int)(coff[c] >> 4);
+            const int idx = m * G + lch[c];
             if constexpr (!XLDS) read_x(m, c, xp[m][c], xq[XS == 2 ? m : 0][XS == 2 ? c : 0]);
             bias[m][c] = sums[2 * idx];
             sx[m][c] = sums[2 * idx + 1];
@@ -406,7 +420,7 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const float t = wave_sum_lane63(acc[m]);
-            if (lane == 63 && n0 + r < N) store_y<YT>(a.y, (size_t)m * N + n0 + r, t);
+            if (lane == 63 && n0 + r < N) store_y<YT>(a.y, blockIdx.y * a.ystride + (size_t)m * N + n0 + r, t);
         }
     }
 }
@@ -414,18 +428,19 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
 template <int M, int CPL, bool XF32, bool SF16, bool ZU, bool BLK>
 void launch_y(const GemvArgs& a, int y_dtype) {
     constexpr int R = gemv_rows(M, CPL);
-    const int G = a.K / 32;
+    const int G = a.slice_chunks;
     const size_t lds = (size_t)M * G * 16 * 4 * (XF32 ? 2 : 1) + (size_t)M * G * 2 * 4;
-    const int grid = (a.N + 4 * R - 1) / (4 * R);  // one batch of rows per wave
+    // one batch of rows per wave; one block row per K slice
+    const dim3 grid((a.N + 4 * R - 1) / (4 * R), (a.Gt + G - 1) / G);
     switch (y_dtype) {
     case BYHIP_F32:
-        hipLaunchKernelGGL((q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_F32>), dim3(grid), dim3(256), lds, stream(), a);
+        launch("q4_gemv", (q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_F32>), grid, dim3(256), lds, a);
         break;
     case BYHIP_F16:
-        hipLaunchKernelGGL((q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_F16>), dim3(grid), dim3(256), lds, stream(), a);
+        launch("q4_gemv", (q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_F16>), grid, dim3(256), lds, a);
         break;
     default:
-        hipLaunchKernelGGL((q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_BF16>), dim3(grid), dim3(256), lds, stream(), a);
+        launch("q4_gemv", (q4_gemv<M, CPL, XF32, SF16, ZU, BLK, BYHIP_BF16>), grid, dim3(256), lds, a);
         break;
     }
     BYHIP_LAUNCHED("q4_gemv");
@@ -470,6 +485,21 @@ int gemv_cpl(int K) {
     return cpl;
 }
 
+// The GEMV's K slices. One slice holds all of K when the per-lane register tile (8 chunks of 32
+// values per lane: 512 chunks) and the block's staging take it: with fp32 activations each staged
+// chunk needs 136 bytes of the 64 KB of LDS (481 chunks, K = 15,392). Longer rows are cut into
+// equal slices that do fit; each slice's blocks write fp32 partial sums and splitk_sum adds them
+// in slice order.
+struct GemvSlices {
+    int slices, chunks;
+};
+GemvSlices gemv_slices(int K, int x_dtype) {
+    const int G = K / 32, maxc = x_dtype == BYHIP_F32 ? 481 : 512;
+    if (G <= maxc) return {1, G};
+    const int s = (G + maxc - 1) / maxc;
+    return {s, (G + s - 1) / s};
+}
+
 // ---- fused decode GEMV (sessionMatmulQ4Fused, gpubackend.nim:3185-3231) ----------------------
 //
 // M = 1, fp32 input and outputs, resident weights with the blocked scale copy. The shader it
@@ -489,6 +519,7 @@ struct FusedMat {
     float zero_value;
     float* y;
     int N, n_pad, batch0;  // batch0: the first row batch of this matrix in the wave numbering
+    int part_off;          // K slices: this matrix's rows in each slice's plane of partial sums
 };
 
 struct FusedArgs {
@@ -497,6 +528,13 @@ struct FusedArgs {
     const float* gamma;  // null: no RMSNorm
     float eps;
     int K, row_bytes, nmats, batches;
+    // K slices (blockIdx.y): slice z takes chunks z * slice_chunks .. of the Gt chunks. With several
+    // slices the waves store their raw dot products to part[z * pstride + part_off + row], and
+    // block 0 of each slice its sum of a^2 to ssq[z]; fused_finish applies the rest.
+    int Gt, slice_chunks;
+    float* part;
+    float* ssq;
+    size_t pstride;
     FusedMat m[3];
 };
 
@@ -514,7 +552,10 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int K = a.K, G = K >> 5;
+    const int K = a.K, Gt = a.Gt;
+    // this block's K slice: chunks c0 .. c0 + G - 1
+    const int c0 = blockIdx.y * a.slice_chunks;
+    const int G = min(a.slice_chunks, Gt - c0);
     // chunk idx as four 16-byte pieces, piece t at uint4 index t G + idx (conflict-free reads, as
     // in q4_gemv)
     uint32_t* xh = lds;                                      // [4][G][4] fp16 pairs, high terms
@@ -533,14 +574,18 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     const FusedMat& fm0 = a.m[mi];
     const int n0 = (wb - fm0.batch0) * R;  // first matrix-local row of the wave
 
-    // This lane's chunks (chunks past K are clamped onto the last one and their scale is zeroed).
+    // This lane's chunks of the slice (chunks past its end are clamped onto its last one and their
+    // scale is zeroed): lch is the chunk within the slice (the staging index), coff its byte offset
+    // in the weight row.
     uint32_t coff[CPL];
+    int lch[CPL];
     bool cv[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int ci = lane + kWave * c;
         cv[c] = ci < G;
-        coff[c] = (uint32_t)min(ci, G - 1) * 16u;
+        lch[c] = min(ci, G - 1);
+        coff[c] = (uint32_t)(c0 + lch[c]) * 16u;
     }
 
     // 1. the first input chunk this thread stages (chunk tid; chunk tid + 256 follows after the
@@ -554,7 +599,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)K * 4u);
     const rsrc_t gr = make_rsrc(a.gamma ? a.gamma : a.x, a.gamma ? (uint32_t)K * 4u : 0u);
     auto load_chunk = [&](int idx, uint4* xraw, uint4* graw) {
-        const uint32_t base = idx < G ? (uint32_t)idx * 128u + 64u * (uint32_t)hf : kOutOfRange;
+        const uint32_t base = idx < G ? (uint32_t)(c0 + idx) * 128u + 64u * (uint32_t)hf : kOutOfRange;
 #pragma unroll
         for (int t = 0; t < XW; ++t) xraw[t] = buf_load16(xr, base == kOutOfRange ? kOutOfRange : base + 16u * t);
         if (a.gamma) {
@@ -571,12 +616,12 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
 #pragma unroll
     for (int j = 0; j < NM; ++j) {
         const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
-        const rsrc_t sr = make_rsrc(fm.sblk, (uint32_t)fm.n_pad * (uint32_t)G * SB);
-        const rsrc_t zr = make_rsrc(ZU ? fm.sblk : fm.zblk, ZU ? 0u : (uint32_t)fm.n_pad * (uint32_t)G * 4u);
+        const rsrc_t sr = make_rsrc(fm.sblk, (uint32_t)fm.n_pad * (uint32_t)Gt * SB);
+        const rsrc_t zr = make_rsrc(ZU ? fm.sblk : fm.zblk, ZU ? 0u : (uint32_t)fm.n_pad * (uint32_t)Gt * 4u);
         const int nb = min(n0, fm.n_pad - R);  // R divides 8 and n0, so the rows sit in one block of 8
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const uint32_t e = ((uint32_t)(nb >> 3) * (uint32_t)G + (coff[c] >> 4)) * 8u + (uint32_t)(nb & 7);
+            const uint32_t e = ((uint32_t)(nb >> 3) * (uint32_t)Gt + (uint32_t)(c0 + lch[c])) * 8u + (uint32_t)(nb & 7);
             uint32_t sw[R * SB / 4];
             load_bytes<R * SB>(sr, e * SB, sw);
 #pragma unroll
@@ -688,6 +733,8 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
             const float t = (ssq_part[lane] + ssq_part[lane + 64]) + (ssq_part[lane + 128] + ssq_part[lane + 192]);
             const float total = wave_sum_lane63(t);
             inv = 1.0f / sqrtf(total / (float)K + a.eps);  // meaningful on lane 63, which stores
+            // K slices: the slice's sum of a^2, once per slice
+            if (a.part && blockIdx.x == 0 && tid == 63) a.ssq[blockIdx.y] = total;
         }
     };
     if constexpr (!TWO) norm_factor();
@@ -710,7 +757,7 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
             const FusedMat& fm = MODE == 1 ? a.m[j] : fm0;
 #pragma unroll
             for (int c = decltype(c_lo)::value; c < decltype(c_hi)::value; ++c) {
-                const int idx = (int)(coff[c] >> 4);
+                const int idx = lch[c];
                 const uint4* sh = reinterpret_cast<const uint4*>(xh) + idx;
                 const uint4* sl = reinterpret_cast<const uint4*>(xl) + idx;
                 const float sxc = sums[idx], fac = facs[idx];
@@ -766,7 +813,16 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     for (int j = 0; j < NM; ++j)
 #pragma unroll
         for (int r = 0; r < R; ++r) dots[j][r] = wave_sum_lane63(acc[j][r]);
-    if (lane == 63) {
+    if (lane == 63 && a.part) {
+        float* pp = a.part + blockIdx.y * a.pstride;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = n0 + r;
+            if (row >= fm0.N) continue;
+#pragma unroll
+            for (int j = 0; j < NM; ++j) pp[(MODE == 1 ? a.m[j].part_off : fm0.part_off) + row] = dots[j][r];
+        }
+    } else if (lane == 63) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int row = n0 + r;
@@ -782,13 +838,48 @@ __global__ __launch_bounds__(256) void q4_gemv_fused(FusedArgs a) {
     }
 }
 
+// The end of a K-sliced fused GEMV: for every output row (the matrices' rows one after another),
+// the slices' dot products added in slice order, scaled by the norm factor from the slices' sums
+// of a^2 (added in slice order), then silu(gate) * up in mode 1 and the residual, as the unsliced
+// kernel's epilogue does.
+template <int MODE>
+__global__ __launch_bounds__(256) void fused_finish(FusedArgs a, int slices, int rows) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows) return;
+    int mi = 0;
+    if (MODE == 0) {
+        if (a.nmats > 1 && i >= a.m[1].part_off) mi = 1;
+        if (a.nmats > 2 && i >= a.m[2].part_off) mi = 2;
+    }
+    const FusedMat& fm = a.m[mi];
+    const int row = i - fm.part_off;
+    float inv = 1.0f;
+    if (a.gamma) {
+        float total = 0.0f;
+        for (int z = 0; z < slices; ++z) total += a.ssq[z];
+        inv = 1.0f / sqrtf(total / (float)a.K + a.eps);
+    }
+    float d = 0.0f, u = 0.0f;
+    for (int z = 0; z < slices; ++z) {
+        d += a.part[z * a.pstride + i];
+        if (MODE == 1) u += a.part[z * a.pstride + a.m[1].part_off + row];
+    }
+    float v = d * inv;
+    if (MODE == 1) {
+        u *= inv;
+        v = v / (1.0f + expf(-v)) * u;
+    }
+    if (a.res) v += a.res[row];
+    fm.y[row] = v;
+}
+
 template <int CPL, int MODE>
 void launch_fused_sz(const FusedArgs& a, bool sf16, bool zu) {
-    const int G = a.K / 32;
+    const int G = a.slice_chunks;
     const size_t lds = (size_t)G * 16 * 4 * 2 + (size_t)G * 4 * 2 + 256 * 4;
-    const dim3 grid((a.batches + 3) / 4);
+    const dim3 grid((a.batches + 3) / 4, (a.Gt + G - 1) / G);
 #define BYHIP_FUSED_CASE(SF, ZU_) \
-    if (sf16 == SF && zu == ZU_) { hipLaunchKernelGGL((q4_gemv_fused<CPL, SF, ZU_, MODE>), grid, dim3(256), lds, stream(), a); }
+    if (sf16 == SF && zu == ZU_) { launch("q4_gemv_fused", (q4_gemv_fused<CPL, SF, ZU_, MODE>), grid, dim3(256), lds, a); }
     BYHIP_FUSED_CASE(true, true)
     else BYHIP_FUSED_CASE(true, false)
     else BYHIP_FUSED_CASE(false, true)
@@ -803,7 +894,8 @@ void launch_fused_sz(const FusedArgs& a, bool sf16, bool zu) {
 // tile (rows x chunks per lane x fp16 terms <= 8, except a single row, which then reads them from
 // LDS), the block's staging (at most 512 chunks) and 64 KB of LDS. 0: not even one row fits.
 int gemv_rows_per_launch(int K, int M, int x_dtype) {
-    const int xs = x_dtype == BYHIP_F32 ? 2 : 1, G = K / 32, cpl = gemv_cpl(K);
+    const int G = gemv_slices(K, x_dtype).chunks;
+    const int xs = x_dtype == BYHIP_F32 ? 2 : 1, cpl = gemv_cpl(G * 32);
     for (int m = std::min(M, 4); m >= 1; --m) {
         const size_t lds = (size_t)m * G * (64 * xs + 8);
         if ((m == 1 || m * xs * cpl <= 8) && m * G <= 512 && lds <= 65536) return m;
@@ -811,23 +903,36 @@ int gemv_rows_per_launch(int K, int M, int x_dtype) {
     return 0;
 }
 
-bool q4_gemv_eligible(const byhip_q4w* w, int M, int x_dtype) {
+bool q4_gemv_eligible(const byhip_q4w* w, int M, int x_dtype, size_t work_bytes) {
     if (w->K % 32 != 0 || (w->group != 0 && w->group % 32 != 0)) return false;
-    const int cpl = gemv_cpl(w->K);
     // 32-bit buffer offsets (below the out-of-range marker) for weights, scales and activations
     const uint64_t lim = kOutOfRange - 64;
     const bool fits = (uint64_t)w->N * w->row_bytes < lim && (uint64_t)(w->N + 8) * (w->K / 32 + w->gpr) * 4 < lim &&
                       (uint64_t)4 * w->K * 4 < lim;
     const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0;
-    return fits && aligned && cpl <= 8 && gemv_rows_per_launch(w->K, M, x_dtype) > 0;
+    // the partial sums of a sliced K fit the scratch
+    const GemvSlices sl = gemv_slices(w->K, x_dtype);
+    const bool room = sl.slices == 1 || (size_t)sl.slices * splitk_stride(M, w->N) * sizeof(float) <= work_bytes;
+    return fits && aligned && room && gemv_rows_per_launch(w->K, M, x_dtype) > 0;
 }
 
-void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
-    const int cpl = gemv_cpl(w->K);
+void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M, void* work,
+                    size_t work_bytes) {
+    const GemvSlices sl = gemv_slices(w->K, x_dtype);
+    const int cpl = gemv_cpl(sl.chunks * 32);
     const size_t xb = dtype_bytes(x_dtype), yb = dtype_bytes(y_dtype);
     const bool blk = w->sblk != nullptr;
     const int step = gemv_rows_per_launch(w->K, M, x_dtype);
     if (step < 1) fail("byhip: internal: GEMV launched on a shape it does not take (K=%d)", w->K);
+    // several slices: fp32 partials [slice][M][N] in the scratch, then splitk_sum into y
+    float* part = nullptr;
+    if (sl.slices > 1) {
+        part = static_cast<float*>(work ? work : workspace());
+        const size_t room = work ? work_bytes : kWorkspaceBytes;
+        if ((size_t)sl.slices * splitk_stride(M, w->N) * sizeof(float) > room)
+            fail("byhip: internal: GEMV partial sums exceed the scratch");
+    }
+    const int yd = part ? BYHIP_F32 : y_dtype;
     for (int m0 = 0; m0 < M; m0 += step) {
         const int mm = std::min(step, M - m0);
         GemvArgs a;
@@ -836,28 +941,53 @@ void launch_q4_gemv(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
         a.scales = blk ? w->sblk : w->scales;
         a.zeros = blk ? w->zblk : w->zeros;
         a.zero_value = w->zero_value;
-        a.y = static_cast<uint8_t*>(y) + (size_t)m0 * w->N * yb;
+        a.y = part ? static_cast<void*>(part + (size_t)m0 * w->N) : static_cast<uint8_t*>(y) + (size_t)m0 * w->N * yb;
         a.K = w->K; a.N = w->N; a.gpr = w->gpr; a.row_bytes = (int)w->row_bytes;
         a.group_chunks = w->group / 32;
         a.n_pad = (w->N + 7) / 8 * 8;
+        a.Gt = w->K / 32; a.slice_chunks = sl.chunks; a.ldx = w->K;
+        a.ystride = part ? splitk_stride(M, w->N) : 0;
         if (x_dtype == BYHIP_F32) {
             switch (mm) {
-            case 1: launch_cpl<1, true>(cpl, a, w, blk, y_dtype); break;
-            case 2: launch_cpl<2, true>(cpl, a, w, blk, y_dtype); break;
-            case 3: launch_cpl<3, true>(cpl, a, w, blk, y_dtype); break;
-            default: launch_cpl<4, true>(cpl, a, w, blk, y_dtype); break;
+            case 1: launch_cpl<1, true>(cpl, a, w, blk, yd); break;
+            case 2: launch_cpl<2, true>(cpl, a, w, blk, yd); break;
+            case 3: launch_cpl<3, true>(cpl, a, w, blk, yd); break;
+            default: launch_cpl<4, true>(cpl, a, w, blk, yd); break;
             }
         } else {
             switch (mm) {
-            case 1: launch_cpl<1, false>(cpl, a, w, blk, y_dtype); break;
-            case 2: launch_cpl<2, false>(cpl, a, w, blk, y_dtype); break;
-            case 3: launch_cpl<3, false>(cpl, a, w, blk, y_dtype); break;
-            default: launch_cpl<4, false>(cpl, a, w, blk, y_dtype); break;
+            case 1: launch_cpl<1, false>(cpl, a, w, blk, yd); break;
+            case 2: launch_cpl<2, false>(cpl, a, w, blk, yd); break;
+            case 3: launch_cpl<3, false>(cpl, a, w, blk, yd); break;
+            default: launch_cpl<4, false>(cpl, a, w, blk, yd); break;
             }
         }
     }
+    if (part) {
+        GemmArgs ga;
+        ga.M = M; ga.N = w->N; ga.y = y; ga.y_dtype = y_dtype; ga.part = part;
+        launch_splitk_sum(ga, sl.slices);
+    }
 }
 
+
+// The fused GEMV's K slices: one when a block stages the whole input (fp16 hi/lo pairs and chunk
+// sums, 136 bytes per chunk, with the norm partials in 64 KB of LDS: 474 chunks; gate and up keep
+// at most 4 chunks per lane: 256), else equal slices that fit.
+GemvSlices fused_slices(int K, int mode) {
+    const int G = K / 32, maxc = mode == 1 ? 256 : 474;
+    if (G <= maxc) return {1, G};
+    const int s = (G + maxc - 1) / maxc;
+    return {s, (G + s - 1) / s};
+}
+
+// Floats of one slice's plane of partial dot products: every matrix's rows (gate then up in mode 1),
+// 16-byte aligned.
+size_t fused_rows_total(const byhip_q4w* const* ws, int n_ws) {
+    size_t rows = 0;
+    for (int i = 0; i < n_ws; ++i) rows += ws[i]->N;
+    return (rows + 3) & ~(size_t)3;
+}
 
 int q4_fused_check(int mode, const byhip_q4w* const* ws, int n_ws) {
     if (mode != 0 && mode != 1) return BYHIP_UNSUPPORTED;
@@ -877,20 +1007,28 @@ int q4_fused_check(int mode, const byhip_q4w* const* ws, int n_ws) {
     }
     if (w0->K % 32 != 0 || (w0->group != 0 && w0->group % 32 != 0)) return BYHIP_UNSUPPORTED;
     if (mode == 1 && ws[1]->N != w0->N) return BYHIP_UNSUPPORTED;
-    // chunks per lane: 8 at most (4 with gate and up); the staged input fits 64 KB of LDS
-    const int G = w0->K / 32;
-    if (gemv_cpl(w0->K) > (mode == 1 ? 4 : 8) || (size_t)G * 136 + 1024 > 65536) return BYHIP_UNSUPPORTED;
+    // a sliced K's partial sums and sums of squares fit the workspace
+    const GemvSlices sl = fused_slices(w0->K, mode);
+    if (sl.slices > 1 && (size_t)sl.slices * (fused_rows_total(ws, n_ws) + 1) * sizeof(float) > kWorkspaceBytes)
+        return BYHIP_UNSUPPORTED;
     return BYHIP_OK;
 }
 
 void launch_q4_gemv_fused(int mode, const float* x, const byhip_q4w* const* ws, int n_ws, float* const* outs,
                           const float* res, const float* gamma, float eps) {
     FusedArgs a{};
-    const int cpl = gemv_cpl(ws[0]->K);
+    const GemvSlices sl = fused_slices(ws[0]->K, mode);
+    const int cpl = gemv_cpl(sl.chunks * 32);
     const int rows = fused_rows(cpl);
     a.x = x; a.res = res; a.gamma = gamma; a.eps = eps;
     a.K = ws[0]->K; a.row_bytes = (int)ws[0]->row_bytes; a.nmats = n_ws;
-    int batches = 0;
+    a.Gt = ws[0]->K / 32; a.slice_chunks = sl.chunks;
+    if (sl.slices > 1) {
+        a.pstride = fused_rows_total(ws, n_ws);
+        a.part = static_cast<float*>(workspace());
+        a.ssq = a.part + (size_t)sl.slices * a.pstride;
+    }
+    int batches = 0, off = 0;
     for (int i = 0; i < n_ws; ++i) {
         const byhip_q4w* w = ws[i];
         FusedMat& m = a.m[i];
@@ -898,6 +1036,8 @@ void launch_q4_gemv_fused(int mode, const float* x, const byhip_q4w* const* ws, 
         m.y = mode == 1 ? outs[0] : outs[i];
         m.N = w->N; m.n_pad = (w->N + 7) / 8 * 8;
         m.batch0 = mode == 1 ? 0 : batches;
+        m.part_off = off;
+        off += w->N;
         if (mode == 0 || i == 0) batches += (w->N + rows - 1) / rows;
     }
     a.batches = batches;
@@ -906,7 +1046,15 @@ void launch_q4_gemv_fused(int mode, const float* x, const byhip_q4w* const* ws, 
     case 1: mode ? launch_fused_sz<1, 1>(a, sf, zu) : launch_fused_sz<1, 0>(a, sf, zu); break;
     case 2: mode ? launch_fused_sz<2, 1>(a, sf, zu) : launch_fused_sz<2, 0>(a, sf, zu); break;
     case 4: mode ? launch_fused_sz<4, 1>(a, sf, zu) : launch_fused_sz<4, 0>(a, sf, zu); break;
-    default: launch_fused_sz<8, 0>(a, sf, zu); break;  // mode 1 stops at 4 (q4_fused_check)
+    default: launch_fused_sz<8, 0>(a, sf, zu); break;  // mode 1 slices stop at 4 chunks per lane
+    }
+    if (sl.slices > 1) {
+        const int out_rows = mode == 1 ? ws[0]->N : off;
+        const dim3 grid((unsigned)((out_rows + 255) / 256));
+        if (mode == 1)
+            launch("fused_finish", fused_finish<1>, grid, dim3(256), 0, a, sl.slices, out_rows);
+        else
+            launch("fused_finish", fused_finish<0>, grid, dim3(256), 0, a, sl.slices, out_rows);
     }
 }
 

@@ -7,8 +7,11 @@
 #include <cstdarg>
 #include <cstdlib>
 #include <cstdint>
+#include <functional>
 #include <stdexcept>
 #include <string>
+#include <tuple>
+#include <utility>
 #include <vector>
 
 #include "byhip.h"
@@ -33,6 +36,38 @@ void check_hip(hipError_t e, const char* what, const char* file, int line);
 #define BYHIP_LAUNCHED(name) ::byhip::check_hip(hipGetLastError(), name, __FILE__, __LINE__)
 
 void set_error(const std::string& msg);
+
+hipStream_t stream();
+
+// A kernel launch kept with its arguments by value, run on the stream it is given.
+using Relaunch = std::function<void(hipStream_t)>;
+// Whether the open session is recorded for direct replay: its launches are then kept (keep_launch)
+// instead of queued, run in order when the session ends, and run again at every replay.
+bool keeping_launches();
+void keep_launch(Relaunch l);
+
+template <typename... P, std::size_t... I>
+void launch_tuple(const char* name, void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                  std::tuple<P...>& t, std::index_sequence<I...>) {
+    void* argv[sizeof...(P) + 1] = {static_cast<void*>(&std::get<I>(t))..., nullptr};
+    check_hip(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, (unsigned)lds, s), name,
+              __FILE__, __LINE__);
+}
+
+// Every kernel of the library is launched through here: on the library stream now, or, inside a
+// session recorded for direct replay, kept for the recording's launches.
+template <typename... P, typename... A>
+void launch(const char* name, void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, A&&... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+    std::tuple<P...> t(static_cast<P>(std::forward<A>(args))...);
+    if (keeping_launches()) {
+        keep_launch([=](hipStream_t s) mutable {
+            launch_tuple(name, kernel, grid, block, lds, s, t, std::index_sequence_for<P...>{});
+        });
+        return;
+    }
+    launch_tuple(name, kernel, grid, block, lds, stream(), t, std::index_sequence_for<P...>{});
+}
 
 // Every entry point: injected fault first, then the device must be initialised.
 void enter_compute();

@@ -387,9 +387,9 @@ void launch_mxfp4(const uint8_t* x, const uint8_t* x_scales, const uint8_t* w,
     a.per_xcd = (a.tiles + kXcds - 1) / kXcds;
     const dim3 grid(kXcds * a.per_xcd);
     switch (y_dtype) {
-    case BYHIP_F32: hipLaunchKernelGGL(mxfp4_gemm<BYHIP_F32>, grid, dim3(256), 0, stream(), a); break;
-    case BYHIP_F16: hipLaunchKernelGGL(mxfp4_gemm<BYHIP_F16>, grid, dim3(256), 0, stream(), a); break;
-    default: hipLaunchKernelGGL(mxfp4_gemm<BYHIP_BF16>, grid, dim3(256), 0, stream(), a); break;
+    case BYHIP_F32: launch("mxfp4_gemm", mxfp4_gemm<BYHIP_F32>, grid, dim3(256), 0, a); break;
+    case BYHIP_F16: launch("mxfp4_gemm", mxfp4_gemm<BYHIP_F16>, grid, dim3(256), 0, a); break;
+    default: launch("mxfp4_gemm", mxfp4_gemm<BYHIP_BF16>, grid, dim3(256), 0, a); break;
     }
     BYHIP_LAUNCHED("mxfp4_gemm");
 }

@@ -223,7 +223,7 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
     std::vector<int> flags((size_t)cblocks * 8);
     float zero0 = 0.0f;
     try {
-        hipLaunchKernelGGL(q4_classify, dim3(cblocks), dim3(256), 0, stream(), d_sc, d_ze, ng, d_flags);
+        launch("q4_classify", q4_classify, dim3(cblocks), dim3(256), 0, d_sc, d_ze, ng, d_flags);
         BYHIP_LAUNCHED("q4_classify");
         BYHIP_HIP(hipMemcpyAsync(flags.data(), d_flags, flags.size() * sizeof(int), hipMemcpyDeviceToHost, stream()));
         BYHIP_HIP(hipMemcpyAsync(&zero0, d_ze, sizeof(float), hipMemcpyDeviceToHost, stream()));
@@ -288,13 +288,13 @@ byhip_q4w* build_resident_dev(const void* wq_src, bool wq_on_device, const float
                                  stream()));
         const size_t work = std::max(ng, blk ? n_pad * G : (size_t)0);
         const int pblocks = (int)std::min<size_t>((work + 255) / 256, (size_t)compute_units() * 16);
-        hipLaunchKernelGGL(q4_pack_scales, dim3(pblocks), dim3(256), 0, stream(), d_sc, d_ze, N, gpr, group, (int)G,
+        launch("q4_pack_scales", q4_pack_scales, dim3(pblocks), dim3(256), 0, d_sc, d_ze, N, gpr, group, (int)G,
                            (int)sf16, (int)zu, w->scales, w->zeros, w->sblk, w->zblk);
         BYHIP_LAUNCHED("q4_pack_scales");
         if (pf) {
             const size_t pw = std::max(((size_t)N + 15) / 16 * nsub * 128, ((size_t)N + 63) / 64 * nsub * 128);
             const int fblocks = (int)std::min<size_t>((pw + 255) / 256, (size_t)compute_units() * 16);
-            hipLaunchKernelGGL(q4_pack_prefill, dim3(fblocks), dim3(256), 0, stream(), w->wq, row_bytes, d_sc, N, K,
+            launch("q4_pack_prefill", q4_pack_prefill, dim3(fblocks), dim3(256), 0, w->wq, row_bytes, d_sc, N, K,
                                gpr, group, reinterpret_cast<uint32_t*>(w->wpf), static_cast<_Float16*>(w->spf));
             BYHIP_LAUNCHED("q4_pack_prefill");
         }
@@ -330,17 +330,17 @@ void launch_generic_y(const void* x, const byhip_q4w* w, void* y, int y_dtype, i
     const int grid = (w->N + 3) / 4;
     switch (y_dtype) {
     case BYHIP_F32:
-        hipLaunchKernelGGL((q4_generic<XF32, SF16, ZU, BYHIP_F32>), dim3(grid), dim3(256), 0, stream(), x,
+        launch("q4_generic", (q4_generic<XF32, SF16, ZU, BYHIP_F32>), dim3(grid), dim3(256), 0, x,
                            w->wq, w->scales, w->zeros, w->zero_value, y, M, w->K, w->N, w->group,
                            w->gpr, w->row_bytes);
         break;
     case BYHIP_F16:
-        hipLaunchKernelGGL((q4_generic<XF32, SF16, ZU, BYHIP_F16>), dim3(grid), dim3(256), 0, stream(), x,
+        launch("q4_generic", (q4_generic<XF32, SF16, ZU, BYHIP_F16>), dim3(grid), dim3(256), 0, x,
                            w->wq, w->scales, w->zeros, w->zero_value, y, M, w->K, w->N, w->group,
                            w->gpr, w->row_bytes);
         break;
     default:
-        hipLaunchKernelGGL((q4_generic<XF32, SF16, ZU, BYHIP_BF16>), dim3(grid), dim3(256), 0, stream(), x,
+        launch("q4_generic", (q4_generic<XF32, SF16, ZU, BYHIP_BF16>), dim3(grid), dim3(256), 0, x,
                            w->wq, w->scales, w->zeros, w->zero_value, y, M, w->K, w->N, w->group,
                            w->gpr, w->row_bytes);
         break;
@@ -431,7 +431,7 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
         return;
     // The vector kernels read 16-byte words of weights and activations.
     const bool aligned = reinterpret_cast<uintptr_t>(w->wq) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
-    const bool gemv = aligned && q4_gemv_eligible(w, M, x_dtype);
+    const bool gemv = aligned && q4_gemv_eligible(w, M, x_dtype, work ? work_bytes : kWorkspaceBytes);
     if (mode == 3) return launch_generic(x, x_dtype, w, y, y_dtype, M);
     if (mode == 4) return launch_gemm_exact(BFormat::Q4Generic, ga);
     if (mode == 0 && M > 1 && M <= 8 && x_dtype == BYHIP_F32 && !exact && w->f16_safe && aligned &&
@@ -446,8 +446,10 @@ void q4_matmul_impl(const void* x, int x_dtype, const byhip_q4w* w, void* y, int
             launch_q4_wide_exact_weights(ga))
             return;
     }
-    if (gemv && (mode == 1 || (mode == 0 && M <= 8))) return launch_q4_gemv(x, x_dtype, w, y, y_dtype, M);
-    // Decode shapes the GEMV does not take stay on the exact per-element kernel.
+    if (gemv && (mode == 1 || (mode == 0 && M <= 8)))
+        return launch_q4_gemv(x, x_dtype, w, y, y_dtype, M, work, work_bytes);
+    // Decode shapes the GEMV does not take (K or the group not a multiple of 32, unaligned rows or
+    // activations, offsets past 32 bits) stay on the exact per-element kernel.
     if (M <= 8 && mode != 2) return launch_generic(x, x_dtype, w, y, y_dtype, M);
     if (!exact && w->f16_safe && aligned && w->K % 32 == 0)
         return launch_gemm(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic, ga);
@@ -589,7 +591,7 @@ int byhip_q4_matmul_fused(int mode, const float* a, byhip_q4w* const* ws, int n_
         const int n_out = mode == 1 ? 1 : n_ws;
         if (q4_fused_check(mode, ws, n_ws) != BYHIP_OK)
             unsupported("byhip: fused GEMV does not take these weights (K, group, groups per row and "
-                        "scale formats must match, K %% 32 == 0, K <= 8192, equal N for gate and up)");
+                        "scale formats must match, K %% 32 == 0, equal N for gate and up)");
         const int K = ws[0]->K;
         int max_n = 0;
         for (int i = 0; i < n_ws; ++i) max_n = std::max(max_n, ws[i]->N);
@@ -646,9 +648,16 @@ int byhip_debug_unpack_q4(const byhip_q4w* w, uint8_t* codes, float* scales, flo
         float* dz = static_cast<float*>(device_alloc(ng * 4));
         const size_t n = std::max(total, ng);
         const int grid = (int)((n + 255) / 256);
-        hipLaunchKernelGGL(q4_unpack, dim3(grid), dim3(256), 0, stream(), w->wq, w->row_bytes, w->K,
-                           w->N, w->scales, w->scale_f16, w->zeros, w->zero_value, w->sblk, w->zblk,
-                           w->group, w->gpr, dc, ds, dz);
+        try {
+            launch("q4_unpack", q4_unpack, dim3(grid), dim3(256), 0, w->wq, w->row_bytes, w->K,
+                               w->N, w->scales, w->scale_f16, w->zeros, w->zero_value, w->sblk, w->zblk,
+                               w->group, w->gpr, dc, ds, dz);
+        } catch (...) {
+            device_free(dc);
+            device_free(ds);
+            device_free(dz);
+            throw;
+        }
         hipError_t e = hipGetLastError();
         if (e == hipSuccess) e = hipStreamSynchronize(stream());
         if (e == hipSuccess) e = hipMemcpy(codes, dc, total, hipMemcpyDeviceToHost);

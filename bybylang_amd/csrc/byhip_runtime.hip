@@ -39,8 +39,20 @@ struct State {
     double realtime_hz = 0.0;  // rate of the counter the timing marks read
     // record / replay (sessionBeginRecording .. sessionFreeRecording, gpubackend.nim:2502-2552)
     bool recording = false;
-    std::vector<hipGraphExec_t> recordings;  // id -> executable graph (null once freed)
+    // Recordings made while `direct` is set keep their kernel launches (with their arguments) and
+    // replay them by launching them again; the others are HIP graphs.
+    bool direct = false;
+    bool direct_open = false;          // the open recording keeps its launches
+    std::vector<Relaunch> kept;        // launches of the open direct recording
+    struct Recording {
+        hipGraphExec_t exec = nullptr;  // graph recordings
+        std::vector<Relaunch> launches; // direct recordings
+        bool live = false;              // false once freed
+    };
+    std::vector<Recording> recordings;  // id -> recording
     int last_recording = -1;
+    int* gate = nullptr;   // pinned host word the replay gate waits on (hipHostMalloc, coherent)
+    int gate_open = 0;     // value that opens the next gate
 };
 
 State& st() {
@@ -54,6 +66,17 @@ thread_local std::string t_last_error;
 // hipDeviceAttributeWallClockRate) with an ordinary vector store.
 __device__ unsigned long long g_marks[2];
 __global__ void timing_mark(int which) { g_marks[which] = __builtin_amdgcn_s_memrealtime(); }
+
+// Replay gate: one thread waits until the host has stored `open` into a pinned word, or until
+// `max_ticks` of the realtime counter have passed (the wait always ends). A direct replay puts it
+// ahead of its launches and opens it once every launch is queued, so the replayed kernels run back
+// to back however slowly the host launches them (a kernel-trace profiler slows each launch).
+__global__ void replay_gate(const int* word, int open, unsigned long long max_ticks) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != open &&
+           __builtin_amdgcn_s_memrealtime() - t0 < max_ticks)
+        __builtin_amdgcn_s_sleep(8);
+}
 std::atomic<int> g_fault_inject{0};
 
 }  // namespace
@@ -99,6 +122,8 @@ hipStream_t stream() { return st().stream; }
 int compute_units() { return st().prop.multiProcessorCount; }
 void* workspace() { return st().workspace; }
 bool session_open() { return st().session_open || st().recording; }
+bool keeping_launches() { return st().recording && st().direct_open; }
+void keep_launch(Relaunch l) { st().kept.push_back(std::move(l)); }
 const hipDeviceProp_t& device_props() { return st().prop; }
 
 void no_host_sync(const char* what) {
@@ -221,6 +246,8 @@ int byhip_init(int device) {
         BYHIP_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
         s.realtime_hz = khz * 1e3;
         BYHIP_HIP(hipMalloc(&s.workspace, kWorkspaceBytes));
+        BYHIP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.gate), sizeof(int), hipHostMallocCoherent));
+        *s.gate = 0;
         static_scratch_setup(device);
         s.device = device;
         s.inited = true;
@@ -384,27 +411,70 @@ int byhip_session_alloc_scratch(size_t n, void** out) {
     });
 }
 
-// Ends a recorded session: the captured work becomes an executable graph, which is launched once
-// (the session's work happens, as a kept Vulkan command buffer is also submitted) and kept.
+// Launches recording `id` once on the library stream.
+static void launch_recording(State& s, int id) {
+    State::Recording& r = s.recordings[id];
+    if (r.exec) {
+        BYHIP_HIP(hipGraphLaunch(r.exec, s.stream));
+    } else {
+        for (Relaunch& l : r.launches) l(s.stream);
+    }
+}
+
+static bool recording_live(const State& s, int id) {
+    return id >= 0 && id < (int)s.recordings.size() && s.recordings[id].live;
+}
+
+// Holds the stream behind a replay gate while a direct recording's launches are queued, and opens
+// it when it goes out of scope (also when a launch fails). Graph replays need none.
+struct ReplayGate {
+    State& s;
+    bool held = false;
+    ReplayGate(State& st_, bool direct) : s(st_) {
+        if (!direct) return;
+        const int open = ++s.gate_open;
+        const unsigned long long max_ticks = (unsigned long long)(0.2 * s.realtime_hz);  // 200 ms
+        launch("replay_gate", replay_gate, dim3(1), dim3(1), 0, (const int*)s.gate, open, max_ticks);
+        held = true;
+    }
+    ~ReplayGate() {
+        if (held) __atomic_store_n(s.gate, s.gate_open, __ATOMIC_RELEASE);
+    }
+};
+
+static bool is_direct(const State& s, int id) { return s.recordings[id].exec == nullptr; }
+
+// Ends a recorded session: the captured work becomes an executable graph (or, recorded for direct
+// replay, the list of its kept launches), which is launched once (the session's work happens, as
+// a kept Vulkan command buffer is also submitted) and kept.
 static void end_recording(State& s) {
-    hipGraph_t graph = nullptr;
+    State::Recording rec;
+    rec.live = true;
+    const bool direct = s.direct_open;
     s.recording = false;
     s.session_open = false;
-    hipError_t e = hipStreamEndCapture(s.stream, &graph);
-    if (e != hipSuccess || !graph) {
-        (void)hipGetLastError();
-        fail("byhip: the recorded session could not be kept: %s", hipGetErrorString(e));
+    if (direct) {
+        rec.launches.swap(s.kept);
+    } else {
+        hipGraph_t graph = nullptr;
+        hipError_t e = hipStreamEndCapture(s.stream, &graph);
+        if (e != hipSuccess || !graph) {
+            (void)hipGetLastError();
+            fail("byhip: the recorded session could not be kept: %s", hipGetErrorString(e));
+        }
+        e = hipGraphInstantiate(&rec.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) fail("byhip: instantiating the recorded session failed: %s", hipGetErrorString(e));
     }
-    hipGraphExec_t exec = nullptr;
-    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) fail("byhip: instantiating the recorded session failed: %s", hipGetErrorString(e));
-    s.recordings.push_back(exec);
+    s.recordings.push_back(std::move(rec));
     s.last_recording = (int)s.recordings.size() - 1;
-    if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
-    BYHIP_HIP(hipGraphLaunch(exec, s.stream));
-    if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
-    e = hipStreamSynchronize(s.stream);
+    {
+        ReplayGate gate(s, direct);
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+        launch_recording(s, s.last_recording);
+        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+    }
+    hipError_t e = hipStreamSynchronize(s.stream);
     std::vector<void*> frees;
     frees.swap(s.deferred_frees);
     if (e != hipSuccess) fail("byhip: session failed on the device: %s", hipGetErrorString(e));
@@ -456,9 +526,12 @@ int byhip_session_recover(void) {
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (s.recording) {
-            hipGraph_t g = nullptr;
-            (void)hipStreamEndCapture(s.stream, &g);
-            if (g) (void)hipGraphDestroy(g);
+            if (!s.direct_open) {
+                hipGraph_t g = nullptr;
+                (void)hipStreamEndCapture(s.stream, &g);
+                if (g) (void)hipGraphDestroy(g);
+            }
+            s.kept.clear();
             s.recording = false;
         }
         (void)hipStreamSynchronize(s.stream);
@@ -509,7 +582,9 @@ int byhip_session_begin_recording(void) {
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (s.session_open) fail("byhip: a session is already open");
-        BYHIP_HIP(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+        s.direct_open = s.direct;
+        s.kept.clear();
+        if (!s.direct_open) BYHIP_HIP(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
         s.session_open = true;
         s.recording = true;
     });
@@ -517,18 +592,29 @@ int byhip_session_begin_recording(void) {
 
 int byhip_session_last_recording(void) { return st().last_recording; }
 
+int byhip_session_set_direct_replay(int on) {
+    return guard([&] {
+        enter_compute();
+        State& s = st();
+        std::lock_guard<std::recursive_mutex> lk(s.mu);
+        s.direct = on != 0;
+    });
+}
+
 int byhip_session_replay(int id, int times) {
     return guard([&] {
         enter_compute();
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (s.session_open) fail("byhip: replay runs outside a session");
-        if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id])
-            fail("byhip: no recording %d", id);
+        if (!recording_live(s, id)) fail("byhip: no recording %d", id);
         if (times < 1) fail("byhip: replay count %d", times);
-        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
-        for (int i = 0; i < times; ++i) BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
-        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        {
+            ReplayGate gate(s, is_direct(s, id));
+            if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+            for (int i = 0; i < times; ++i) launch_recording(s, id);
+            if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        }
         BYHIP_HIP(hipStreamSynchronize(s.stream));
         if (s.timing) {
             float ms = 0.0f;
@@ -545,14 +631,17 @@ int byhip_session_replay_after(int pre_id, int pre_times, int id, int times) {
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (s.session_open) fail("byhip: replay runs outside a session");
         for (int r : {pre_id, id})
-            if (r < 0 || r >= (int)s.recordings.size() || !s.recordings[r]) fail("byhip: no recording %d", r);
+            if (!recording_live(s, r)) fail("byhip: no recording %d", r);
         if (pre_times < 1 || times < 1) fail("byhip: replay counts %d, %d", pre_times, times);
         // Everything is queued before the first wait: while the lead-in runs, the host has already
         // queued the begin event and the timed launches behind it.
-        for (int i = 0; i < pre_times; ++i) BYHIP_HIP(hipGraphLaunch(s.recordings[pre_id], s.stream));
-        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
-        for (int i = 0; i < times; ++i) BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
-        if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        {
+            ReplayGate gate(s, is_direct(s, pre_id) || is_direct(s, id));
+            for (int i = 0; i < pre_times; ++i) launch_recording(s, pre_id);
+            if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_begin, s.stream));
+            for (int i = 0; i < times; ++i) launch_recording(s, id);
+            if (s.timing) BYHIP_HIP(hipEventRecord(s.ev_end, s.stream));
+        }
         BYHIP_HIP(hipStreamSynchronize(s.stream));
         if (s.timing) {
             float ms = 0.0f;
@@ -590,7 +679,7 @@ int byhip_session_mark(int which) {
         if (which != 0 && which != 1) fail("byhip: mark %d (0: begin, 1: end)", which);
         if (!s.recording && s.session_open) fail("byhip: marks go into a recording or outside a session");
         if (!s.recording && which == 0) clear_marks(s);
-        hipLaunchKernelGGL(timing_mark, dim3(1), dim3(1), 0, s.stream, which);
+        launch("timing_mark", timing_mark, dim3(1), dim3(1), 0, which);
         BYHIP_LAUNCHED("timing_mark");
     });
 }
@@ -611,9 +700,12 @@ int byhip_session_replay_marked(int id) {
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
         if (s.session_open) fail("byhip: replay runs outside a session");
-        if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id]) fail("byhip: no recording %d", id);
+        if (!recording_live(s, id)) fail("byhip: no recording %d", id);
         clear_marks(s);
-        BYHIP_HIP(hipGraphLaunch(s.recordings[id], s.stream));
+        {
+            ReplayGate gate(s, is_direct(s, id));
+            launch_recording(s, id);
+        }
         char what[48];
         snprintf(what, sizeof what, "recording %d", id);
         take_marks(s, what);
@@ -625,10 +717,11 @@ int byhip_session_free_recording(int id) {
         enter_compute();
         State& s = st();
         std::lock_guard<std::recursive_mutex> lk(s.mu);
-        if (id < 0 || id >= (int)s.recordings.size() || !s.recordings[id]) return;
+        if (!recording_live(s, id)) return;
         BYHIP_HIP(hipStreamSynchronize(s.stream));
-        BYHIP_HIP(hipGraphExecDestroy(s.recordings[id]));
-        s.recordings[id] = nullptr;
+        State::Recording& r = s.recordings[id];
+        if (r.exec) BYHIP_HIP(hipGraphExecDestroy(r.exec));
+        r = State::Recording();
     });
 }
 
@@ -677,7 +770,7 @@ extern "C" int byhip_debug_read(const void* src, size_t bytes, void* sink, size_
         check_span(src, bytes, "read source");
         check_span(sink, (size_t)grid * 4 * sizeof(uint32_t), "read sink");
         if (bytes == 0) return;
-        hipLaunchKernelGGL(read_words, dim3(grid), dim3(256), 0, stream(), static_cast<const uint4*>(src),
+        launch("read_words", read_words, dim3(grid), dim3(256), 0, static_cast<const uint4*>(src),
                            bytes / 16, static_cast<uint32_t*>(sink));
         BYHIP_LAUNCHED("read_words");
     });
@@ -693,7 +786,7 @@ extern "C" int byhip_debug_copy(void* dst, const void* src, size_t bytes) {
         const size_t n = bytes / 16;
         const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, (size_t)compute_units() * 16);
         if (n == 0) return;
-        hipLaunchKernelGGL(copy_words, dim3(grid), dim3(256), 0, stream(), static_cast<const uint4*>(src),
+        launch("copy_words", copy_words, dim3(grid), dim3(256), 0, static_cast<const uint4*>(src),
                            static_cast<uint4*>(dst), n);
         BYHIP_LAUNCHED("copy_words");
     });

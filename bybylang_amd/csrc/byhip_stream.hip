@@ -1,0 +1,271 @@
+// byhip_stream.hip - the small-M streaming Q4 GEMM (gfx950): y[M, N] = x[M, K] . W^T for 9 .. 32
+// rows of fp16 activations on resident weights with the prefill copy (cpu_kernels_impl.inc:293-319
+// semantics; each weight rounded once to fp16, fp32 accumulation in v_mfma_f32_16x16x32_f16).
+//
+// At small M the weights dominate the bytes, and a GEMM tile that covers only part of K (split-K)
+// pays a second launch for the partial sums, while a tile that covers all of K but few columns
+// leaves most CUs idle. Here one block per CU owns a strip of 16 FN output columns over the whole
+// K, so every weight byte streams from HBM once and the grid fills the chip at any N:
+//   Block: eight waves (two per SIMD). Wave w takes the block's 64-value sub-steps w, w + 8, ...
+//   for all BM rows and all FN column fragments, with private LDS buffers, so the K loop has no
+//   block barrier; the eight partial tiles are added in wave order at the end.
+//   Per sub-step a wave moves the BM activation rows' 128-byte slices straight into one of its
+//   four LDS buffers (1 KB direct loads, whole lines, XOR-swizzled as in the wide tile so the
+//   fragment reads are free of bank conflicts), loads each fragment's 512 contiguous bytes of the
+//   prefill copy (8 bytes per lane) and its fp16 scale, three sub-steps ahead.
+//   The activations are the same for every block and come from L2: per CU that is BM x K x 2 bytes
+//   (256 KB at M = 32, K = 4096), the bound at small N; at large N the weights stream at the HBM
+//   rate.
+#include <algorithm>
+
+#include "byhip_gemm.h"
+#include "byhip_internal.h"
+#include "byhip_kernels.h"
+
+namespace byhip {
+namespace {
+
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+constexpr int kStreamWaves = 8;  // per block, one block per CU
+constexpr int kStreamDepth = 4;  // LDS buffers and register sets per wave: loads three sub-steps ahead
+constexpr int kSub = 64;         // K values per sub-step (the prefill copy's unit)
+constexpr int kMaxFN = 8;        // column fragments per block
+
+template <int FM, int FN>
+struct StreamShape {
+    static constexpr int kBM = 16 * FM;
+    static constexpr int kXBuf = kBM * kSub * 2;        // one sub-step's activation slices
+    static constexpr int kXLoads = kBM / 8;             // 1 KB direct loads per sub-step
+    static constexpr int kLoads = kXLoads + 2 * FN;     // with the weights and the scales
+    static constexpr int kLdsX = kStreamWaves * kStreamDepth * kXBuf;
+    static constexpr int kPitch = 16 * FN + 4;          // floats per row of a staged partial tile
+    static constexpr int kLdsRed = kStreamWaves * kBM * kPitch * 4;
+    static constexpr int kLds = kLdsX > kLdsRed ? kLdsX : kLdsRed;
+};
+
+// One wave's weights of one sub-step: per fragment 16 nibbles (two words) and the fp16 scale of the
+// lane's 32-value group.
+template <int FN>
+struct StreamW {
+    v2u w[FN];
+    uint32_t s[FN];
+};
+
+template <int FM, int FN, int YT>
+__global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
+    using S = StreamShape<FM, FN>;
+    constexpr int D = kStreamDepth, BM = S::kBM, L = S::kLoads;
+    static_assert(S::kLds <= 160 * 1024 && (D - 1) * L <= 63,
+                  "q4_gemm_stream: the buffers must fit LDS and the loads in flight the wait counter");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
+
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int f0 = blockIdx.x * FN;  // the block's first column fragment
+    const int K = a.K;
+    const uint32_t nsub_all = (uint32_t)K / kSub;
+    const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
+    const int nsub = a.part ? min(a.split_steps, (int)nsub_all - s_first) : (int)nsub_all;
+    const int nt = nsub > w ? (nsub - w + kStreamWaves - 1) / kStreamWaves : 0;  // this wave's sub-steps
+
+    // Rows past M, fragments past N and sub-steps past the wave's last read zeros through the range
+    // checks (the launcher keeps every offset below 2^31).
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
+    const rsrc_t wr = make_rsrc(a.wpf, (uint32_t)(((size_t)a.N + 15) / 16 * nsub_all * 512));
+    const rsrc_t sr = make_rsrc(a.spf, (uint32_t)(((size_t)a.N + 63) / 64 * nsub_all * 256));
+    // Direct load q: rows 8 q + lane / 8, LDS slot lane % 8 holding chunk (lane % 8) ^ x_swizzle(row).
+    uint32_t xo[S::kXLoads];
+#pragma unroll
+    for (int q = 0; q < S::kXLoads; ++q) {
+        const int r = 8 * q + (lane >> 3), chunk = (lane & 7) ^ x_swizzle(r);
+        xo[q] = (uint32_t)r * (uint32_t)K * 2u + 16u * chunk;
+    }
+    const uint32_t wfrag = nsub_all * 512u, squad = nsub_all * 256u;
+    // the lane's scale in a quad's [2][16][4] block: its 32-value group g / 2, column c
+    const uint32_t soff = 2u * (4u * (16u * (uint32_t)(g >> 1) + (uint32_t)c));
+    uint8_t* const xw = lds + w * D * S::kXBuf;  // this wave's buffers
+    // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot (2 g + kk) ^ x_swizzle(c).
+    const int rd0 = 128 * c + 16 * ((2 * g) ^ x_swizzle(c)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ x_swizzle(c));
+
+    auto load_x = [&](int t, int buf) __attribute__((always_inline)) {
+        const bool ok = t < nt;
+        const uint32_t u = (uint32_t)(s_first + (ok ? w + kStreamWaves * t : 0));
+        const uint32_t oob = ok ? 0u : 0x80000000u;
+        uint8_t* const dst = xw + buf * S::kXBuf;
+#pragma unroll
+        for (int q = 0; q < S::kXLoads; ++q) lds_dma16(xr, dst + 1024 * q, xo[q], oob + 128u * u);
+    };
+    auto load_ws = [&](StreamW<FN>& r, int t) __attribute__((always_inline)) {
+        const bool ok = t < nt;
+        const uint32_t u = (uint32_t)(s_first + (ok ? w + kStreamWaves * t : 0));
+        const uint32_t oob = ok ? 0u : 0x80000000u;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint32_t f = (uint32_t)(f0 + j);
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, 8u * lane, oob + f * wfrag + 512u * u, 0);
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff + 2u * (f & 3u), oob + (f >> 2) * squad + 256u * u, 0);
+        }
+    };
+
+    const _Float16 zlo = (_Float16)(1024.0f + a.zero_value), zhi = (_Float16)(64.0f + a.zero_value);
+    const h2 zz_lo = {zlo, zlo}, zz_hi = {zhi, zhi};
+    uint32_t mag_lo, mag_hi;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mag_lo));
+    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mag_hi));
+
+    f4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    // (q - zero) * scale in fp16 for MFMA kk (word kk of each fragment): the nibble pairs of the
+    // prefill copy's order come out in natural K order from one AND-OR against the fp16 exponent
+    // words (0x6400 | q is 1024 + q, 0x5400 | q << 4 is 64 + q), the bias and zero go in one exact
+    // subtraction, and the product is rounded once.
+    auto dequant = [&](const StreamW<FN>& r, int kk, h8 (&bw)[FN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const _Float16 sc = bits_h((uint16_t)r.s[j]);
+            const h2 ss = {sc, sc};
+            const uint32_t d = r.w[j][kk], d8 = d >> 8;
+            const h2 q0 = bits_h2((d & 0x000F000Fu) | mag_lo) - zz_lo;
+            const h2 q1 = bits_h2((d & 0x00F000F0u) | mag_hi) - zz_hi;
+            const h2 q2 = bits_h2((d8 & 0x000F000Fu) | mag_lo) - zz_lo;
+            const h2 q3 = bits_h2((d8 & 0x00F000F0u) | mag_hi) - zz_hi;
+            const uint4 u = make_uint4(h2_bits(q0 * ss), h2_bits(q1 * ss), h2_bits(q2 * ss), h2_bits(q3 * ss));
+            bw[j] = *reinterpret_cast<const h8*>(&u);
+        }
+    };
+    auto read_x = [&](int buf, int kk, h8 (&x)[FM]) __attribute__((always_inline)) {
+        const uint8_t* src = xw + buf * S::kXBuf + (kk ? rd1 : rd0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) x[i] = *reinterpret_cast<const h8*>(src + 2048 * i);
+    };
+
+    // Sub-steps 0 .. D - 2 are loaded here, sub-step t + D - 1 in sub-step t into the buffer and
+    // register set that sub-step t - 1 used (its fragment reads and weights were consumed by its
+    // MFMAs). Loads past the wave's last sub-step read zeros, so every sub-step waits for the same
+    // count: the loads of t + 1 .. t + D - 2 may stay in flight.
+    StreamW<FN> rs[D];
+    static_for<D - 1>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        load_x(k, k);
+        load_ws(rs[k], k);
+    });
+    auto step = [&](int t, auto kc) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value, kp = (k + D - 1) % D;
+        wait_vmcnt<(D - 2) * L>();
+        __builtin_amdgcn_sched_barrier(0);
+        load_x(t + D - 1, kp);
+        load_ws(rs[kp], t + D - 1);
+        h8 x0[FM], x1[FM], b0[FN], b1[FN];
+        read_x(k, 0, x0);
+        read_x(k, 1, x1);
+        dequant(rs[k], 0, b0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0[i], b0[j], acc[i][j], 0, 0, 0);
+        dequant(rs[k], 1, b1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1[i], b1[j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int t0 = 0; t0 < nt; t0 += D) {
+        static_for<D>([&](auto kc) {
+            const int t = t0 + decltype(kc)::value;
+            if (t < nt) step(t, kc);
+        });
+    }
+
+    // Partial tiles -> LDS in output layout once every load has landed (those past the last
+    // sub-step wrote zeros into the buffers) and every wave is done with its buffers -> the eight
+    // partials added in wave order -> y or the split-K partials.
+    wait_vmcnt<0>();
+    __syncthreads();
+    constexpr int P = S::kPitch;
+    float* red = reinterpret_cast<float*>(lds);  // [waves][BM rows][P]
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(w * BM + 16 * i + 4 * g + r) * P + 16 * j + c] = acc[i][j][r];
+    __syncthreads();
+    float* part = a.part ? a.part + (size_t)blockIdx.z * splitk_stride(a.M, a.N) : nullptr;
+    const bool vec = out8_vector_ok<YT>(a, part);
+    constexpr int kChunks = BM * 2 * FN;  // 8 outputs each
+    for (int u = threadIdx.x; u < kChunks; u += 512) {
+        const int row = u / (2 * FN), col = (u % (2 * FN)) * 8;
+        if (row >= a.M) continue;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kStreamWaves; ++ww) {
+            const float* src = red + (ww * BM + row) * P + col;
+            const float4 s0 = *reinterpret_cast<const float4*>(src);
+            const float4 s1 = *reinterpret_cast<const float4*>(src + 4);
+            v[0] += s0.x; v[1] += s0.y; v[2] += s0.z; v[3] += s0.w;
+            v[4] += s1.x; v[5] += s1.y; v[6] += s1.z; v[7] += s1.w;
+        }
+        store_out8<YT>(a, part, vec, row, 16 * f0 + col, v);
+    }
+}
+
+template <int FM, int FN>
+void launch_stream_y(const GemmArgs& a, dim3 grid) {
+    switch (a.y_dtype) {
+    case BYHIP_F32: launch("q4_gemm_stream", (q4_gemm_stream<FM, FN, BYHIP_F32>), grid, dim3(512), 0, a); break;
+    case BYHIP_F16: launch("q4_gemm_stream", (q4_gemm_stream<FM, FN, BYHIP_F16>), grid, dim3(512), 0, a); break;
+    default: launch("q4_gemm_stream", (q4_gemm_stream<FM, FN, BYHIP_BF16>), grid, dim3(512), 0, a); break;
+    }
+}
+
+template <int FM>
+void launch_stream_fm(const GemmArgs& a, int fn, dim3 grid) {
+    switch (fn) {
+    case 1: launch_stream_y<FM, 1>(a, grid); break;
+    case 2: launch_stream_y<FM, 2>(a, grid); break;
+    case 3: launch_stream_y<FM, 3>(a, grid); break;
+    case 4: launch_stream_y<FM, 4>(a, grid); break;
+    case 5: launch_stream_y<FM, 5>(a, grid); break;
+    case 6: launch_stream_y<FM, 6>(a, grid); break;
+    case 7: launch_stream_y<FM, 7>(a, grid); break;
+    default: launch_stream_y<FM, 8>(a, grid); break;
+    }
+}
+
+}  // namespace
+
+bool q4_stream_ok(const GemmArgs& a) {
+    constexpr uint64_t kLim = 0x80000000u;  // offsets stay below 2^31 (the kernel's out-of-range steps)
+    return a.x_dtype == BYHIP_F16 && a.wpf && a.spf && a.M >= 1 && a.M <= 32 && a.K % kSub == 0 &&
+           (uint64_t)32 * a.K * 2 < kLim && (uint64_t)(a.N + 16 * kMaxFN) * a.K / 2 < kLim &&
+           (uint64_t)(a.N + 64 * kMaxFN) / 64 * (a.K / kSub) * 256 < kLim;
+}
+
+// Column fragments per block: the fewest that give every CU at most one block (at most 8), so each
+// CU streams one strip of the weights. K is split (fp32 partials, then splitk_sum) only when asked
+// (`split_choice`, or BYHIP_Q4_SPLIT).
+void launch_q4_stream(const GemmArgs& a0, int split_choice) {
+    GemmArgs a = a0;
+    const long cus = compute_units();
+    const long nfr = (a.N + 15) / 16;
+    const int fn = (int)std::min<long>(kMaxFN, std::max<long>(1, (nfr + cus - 1) / cus));
+    const long blocks = (nfr + fn - 1) / fn;
+    const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
+    const int splits = forced > 1 ? choose_split(a, blocks, a.K / kSub, kStreamWaves, forced, 1) : 1;
+    if (splits == 1) a.part = nullptr;
+    const dim3 grid((unsigned)blocks, 1, (unsigned)splits);
+    if (a.M <= 16) launch_stream_fm<1>(a, fn, grid);
+    else launch_stream_fm<2>(a, fn, grid);
+    BYHIP_LAUNCHED("q4_gemm_stream");
+    if (a.part) launch_splitk_sum(a, splits);
+}
+
+}  // namespace byhip

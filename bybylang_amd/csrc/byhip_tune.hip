@@ -267,7 +267,7 @@ PlanEntry tune(const byhip_q4w* w, int M, int x_dtype) {
             float total = 0.0f;
             for (int r = 0; r < reps; ++r) {
                 if (scrub) {
-                    hipLaunchKernelGGL(scrub_read, dim3(kScrubBlocks), dim3(256), 0, stream(),
+                    launch("scrub_read", scrub_read, dim3(kScrubBlocks), dim3(256), 0,
                                        static_cast<const uint4*>(scrub), kScrubBytes / 16,
                                        reinterpret_cast<uint32_t*>(static_cast<char*>(scrub) + kScrubBytes));
                     BYHIP_LAUNCHED("scrub_read");

@@ -5,6 +5,12 @@
         --between-marks only the dispatches that start between the two dispatches of each pair of
         timing marks (the library's timing_mark kernel: bench.py's timed steps)
 
+    python -m bybylang_amd.profile_summary regions DB
+        one table per timed region (the dispatches between the two dispatches of each pair of
+        timing marks, in order: bench.py's configurations in the order it runs them): the region's
+        span from the end of its first mark to the start of its second, and per kernel the dispatch
+        count and average / min / max duration
+
     python -m bybylang_amd.profile_summary traffic --fetch DB --write DB --copy-bytes N
                                                    --kernel SUBSTRING [--json OUT]
         HBM bytes per dispatch of the kernel whose name contains SUBSTRING, from a FETCH_SIZE run
@@ -50,6 +56,23 @@ def kernel_durations_between_marks(db: str):
             per[name].append(en - st)
     out = [(k, len(v), sum(v) / len(v), min(v), max(v)) for k, v in per.items()]
     return sorted(out, key=lambda r: -r[1] * r[2])
+
+
+def kernel_regions(db: str):
+    """[(span ns, [(name, n, avg, min, max), ...]), ...] per pair of timing marks, in time order."""
+    con = sqlite3.connect(db)
+    rows = con.execute("select name, start, end from kernels order by start").fetchall()
+    con.close()
+    marks = [(st, en) for name, st, en in rows if "timing_mark" in name]
+    out = []
+    for (a0, a1), (b0, _) in zip(marks[0::2], marks[1::2]):
+        per = collections.defaultdict(list)
+        for name, st, en in rows:
+            if "timing_mark" not in name and a0 < st < b0:
+                per[name].append(en - st)
+        stats = [(k, len(v), sum(v) / len(v), min(v), max(v)) for k, v in per.items()]
+        out.append((b0 - a1, sorted(stats, key=lambda r: -r[1] * r[2])))
+    return out
 
 
 def counter_per_dispatch(db: str, counter: str):
@@ -118,6 +141,8 @@ def main(argv=None) -> int:
     t = sub.add_parser("trace")
     t.add_argument("db")
     t.add_argument("--between-marks", action="store_true")
+    g = sub.add_parser("regions")
+    g.add_argument("db")
     r = sub.add_parser("traffic")
     r.add_argument("--fetch", required=True)
     r.add_argument("--write", required=True)
@@ -133,6 +158,14 @@ def main(argv=None) -> int:
             print(f"`{name[:110]}`: {vals['dispatches']} dispatches, {vals['avg_us']:.2f} us")
             for k in sorted(v for v in vals if v not in ("dispatches", "avg_us")):
                 print(f"  {k} = {vals[k]:.4g}")
+        return 0
+    if a.cmd == "regions":
+        for i, (span, stats) in enumerate(kernel_regions(a.db)):
+            total = sum(n * avg for _, n, avg, _, _ in stats)
+            print(f"\nRegion {i}: span {span / 1e3:.2f} us, kernel time {total / 1e3:.2f} us\n")
+            print("| kernel | dispatches | avg us | min us | max us |\n|---|---:|---:|---:|---:|")
+            for name, n, avg, mn, mx in stats:
+                print(f"| `{name[:110]}` | {n} | {avg / 1e3:.3f} | {mn / 1e3:.3f} | {mx / 1e3:.3f} |")
         return 0
     if a.cmd == "trace":
         print(f"| kernel | dispatches | avg us | min us | max us |\n|---|---:|---:|---:|---:|")

@@ -145,6 +145,12 @@ int byhip_session_replay_marked(int id);
 int byhip_session_take_marks(void);
 /* sessionFreeRecording. */
 int byhip_session_free_recording(int id);
+/* A measurement switch with no counterpart in the reference: recordings begun while it is on keep
+ * their kernel launches (kernel, launch shape and arguments by value) instead of capturing a HIP
+ * graph; ending one launches them in order, and every replay launches them again, directly on the
+ * library stream. Same results as the graph form; it exists so that profilers which trace direct
+ * dispatches see exactly the replayed kernels (off by default). */
+int byhip_session_set_direct_replay(int on);
 
 /* ── Q4 block-dequant GEMV / GEMM ─────────────────────────────────────────────────────────── */
 

@@ -109,9 +109,8 @@ def test_fused_decode_layer_shapes(hip, oracle):
 @pytest.mark.parametrize("K,Ns,norm", [(10240, [37, 21], True), (14336, [50], True), (12288, [8, 8, 8], False)])
 def test_fused_long_rows(hip, oracle, K, Ns, norm):
     """Rows of more than four chunks per lane (two rows per wave) and inputs staged as two chunks
-    per thread (K > 8192), mode 0; gate * up stays at four chunks per lane and returns
-    BYHIP_UNSUPPORTED beyond."""
-    from bybylang_amd import _abi
+    per thread (K > 8192), mode 0; gate * up keeps four chunks per lane and runs such rows in K
+    slices (the slices' partial dot products and sums of squares finished by a second kernel)."""
     mats, a, gamma, res = make(1400 + K, K, Ns)
     gam = gamma if norm else None
     print(f"fused long rows K={K} Ns={Ns} norm={norm}", flush=True)
@@ -122,13 +121,14 @@ def test_fused_long_rows(hip, oracle, K, Ns, norm):
     if len(Ns) >= 2 and Ns[0] == Ns[1] or len(Ns) == 1:
         pair = [mats[0], mats[0]]
         rc, got = run_fused(hip, 1, pair, a, K, 32, res, gam, 1e-5)
-        assert rc == _abi.BYHIP_UNSUPPORTED
-        assert np.all(got[0] == np.float32(-12345.0))
+        assert rc == 0
+        ref_check(got[0], oracle.q4_fused(1, a, pair, K, 32, K // 32, residual=res, gamma=gam, eps=1e-5)[0])
+        assert np.all(got[1] == np.float32(-12345.0))
 
 
 @pytest.mark.parametrize("case", ["mode1_one_weight", "mode1_three_weights", "four_weights",
                                   "few_outputs", "mode1_one_output", "k_mismatch", "n_mismatch_mode1",
-                                  "long_k", "mode2"])
+                                  "k_not_32", "mode2"])
 def test_fused_unsupported_leaves_outputs(hip, case):
     """The combinations the reference's encoders reject (gpubackend.nim:3200-3206), and weights the
     kernel does not take, return BYHIP_UNSUPPORTED before any work: the outputs keep their contents."""
@@ -146,11 +146,12 @@ def test_fused_unsupported_leaves_outputs(hip, case):
         n_out = 1
     elif case == "n_mismatch_mode1":
         Ns = [16, 24]
-    elif case == "long_k":
-        K = 16384
     elif case == "mode2":
         mode = 2
-    mats, a, _, _ = make(1200, K, Ns)
+    group = 32
+    if case == "k_not_32":  # the kernel reads whole 32-value chunks
+        K, group = 272, 16
+    mats, a, _, _ = make(1200, K, Ns, group)
     if case == "k_mismatch":
         other, _, _, _ = make(1201, 2 * K, [16])
         ws = [hip.Q4Weights(*mats[0][:3], K, 16, 32, K // 32), hip.Q4Weights(*other[0][:3], 2 * K, 16, 32, 2 * K // 32)]
@@ -159,7 +160,7 @@ def test_fused_unsupported_leaves_outputs(hip, case):
         assert rc == _abi.BYHIP_UNSUPPORTED
         assert np.all(outs[0].read(np.float32, 16) == 7.0)
         return
-    rc, got = run_fused(hip, mode, mats, a, K, 32, n_out=n_out)
+    rc, got = run_fused(hip, mode, mats, a, K, group, n_out=n_out)
     assert rc == _abi.BYHIP_UNSUPPORTED
     for o in got:
         assert np.all(o == np.float32(-12345.0))

@@ -21,8 +21,9 @@ pytestmark = pytest.mark.gpu
 def gb(hip):
     from bybylang_amd import gpubackend as g
     yield g
-    # leave no session open for the next test
+    # leave no session open and recordings as HIP graphs for the next test
     g.sessionRecoverQueue(g.gbHip)
+    _abi.check(_abi.load().byhip_session_set_direct_replay(0))
 
 
 def fp4_case(g, M, K, N):
@@ -37,7 +38,11 @@ def fp4_case(g, M, K, N):
     return packed, words, table
 
 
-def test_record_replay_rotating_weights_and_tile_gemm(gb, oracle):
+@pytest.mark.parametrize("direct", [False, True], ids=["graph", "direct"])
+def test_record_replay_rotating_weights_and_tile_gemm(gb, oracle, direct):
+    """As HIP graphs, and with the recording's launches kept and replayed directly
+    (byhip_session_set_direct_replay): the same results either way."""
+    _abi.check(_abi.load().byhip_session_set_direct_replay(int(direct)))
     g = synth.rng(9100)
     M, K, N, copies = 3, 1024, 512, 3
     mats = [synth.q4_weights(g, N, K)[:3] for _ in range(copies)]
@@ -91,9 +96,11 @@ def test_record_replay_rotating_weights_and_tile_gemm(gb, oracle):
         gb.residentFreeQ4(w)
 
 
-def test_waiting_calls_refused_while_recording(gb, hip):
+@pytest.mark.parametrize("direct", [False, True], ids=["graph", "direct"])
+def test_waiting_calls_refused_while_recording(gb, hip, direct):
     """Reads, uploads, frees and syncs wait for the device: refused inside a recording, which
     then still ends, replays and computes."""
+    _abi.check(_abi.load().byhip_session_set_direct_replay(int(direct)))
     g = synth.rng(9200)
     K, N = 256, 64
     wq, sc, ze, _ = synth.q4_weights(g, N, K)
@@ -179,12 +186,15 @@ def test_gpu_seconds(gb):
     gb.residentFreeQ4(w)
 
 
-def test_timing_marks_direct_and_recorded(gb, hip):
+@pytest.mark.parametrize("direct", [False, True], ids=["graph", "direct"])
+def test_timing_marks_direct_and_recorded(gb, hip, direct):
     """The measurement marks (no counterpart in the reference): work launched directly between
     byhip_session_mark(0) and (1) is counted by byhip_session_take_marks, the same work recorded
-    between the two marks by byhip_session_replay_marked; an interval with no end mark and a
-    marked replay of a recording without marks are refused."""
+    between the two marks by byhip_session_replay_marked (recordings as graphs or as kept
+    launches); an interval with no end mark and a marked replay of a recording without marks are
+    refused."""
     lib = _abi.load()
+    _abi.check(lib.byhip_session_set_direct_replay(int(direct)))
     g = synth.rng(9500)
     K, N, n = 4096, 4096, 50
     wq, sc, ze, _ = synth.q4_weights(g, N, K)
