@@ -78,6 +78,7 @@ SIGNATURES = {
     "byhip_session_take_marks": (_I, []),
     "byhip_session_free_recording": (_I, [_I]),
     "byhip_session_set_direct_replay": (_I, [_I]),
+    "byhip_debug_alloc_count": (C.c_ulonglong, []),
     "byhip_q4_resident_upload": (_I, [_U8P, _SZ, _SZ, _FP, _FP, _I, _I, _I, _I, C.POINTER(_VP)]),
     "byhip_q4_resident_from_device": (_I, [_VP, _SZ, _VP, _VP, _I, _I, _I, _I, C.POINTER(_VP)]),
     "byhip_q4_resident_free": (_I, [_VP]),

@@ -139,6 +139,9 @@ void launch_gemm(BFormat fmt, const GemmArgs& a);
 // Whether launch_gemm(Q4Fast, a) takes a call with fp32 activations on the wide tile over two fp16
 // activation planes (the prefill copy's format conditions, and BYHIP_Q4_F32_WIDE not 0).
 bool q4_f32_wide_takes(const GemmArgs& a);
+// Whether launch_gemm(Q4Fast, a) takes the small-M streaming GEMM (fp16 activations, M up to 32 or
+// BYHIP_Q4_SKINNY_MAX_M, the prefill copy; BYHIP_Q4_STREAM=0 switches it off).
+bool q4_stream_takes(const GemmArgs& a);
 // Queues the 16- or 32-row wide tile on fp16 activations with each Q4 weight as two fp16 terms that
 // add up to it exactly (the weights' prefill copy, M <= 32); false, queueing nothing, when it does
 // not take the call.
@@ -153,10 +156,20 @@ void launch_gemm_exact(BFormat fmt, const GemmArgs& a);
 // The Q4 GEMM kernels by explicit choice (a tuned plan's candidates): kQ4Pipe, the LDS-staged
 // pipelined kernel with `tile` 1..4 (64x128, 64x64, 32x128, 32x64) and `splits`; kQ4Skinny (M <= 32,
 // `splits`); kQ4General, the general LDS-staged kernel; kQ4Big, the 128 x 256 prefill tile, and
-// kQ4Wide, the 64 x 128 skinny tile (`splits`). tile / splits 0 keep the default choice.
+// kQ4Wide, the 64 x 128 skinny tile (`splits`); kQ4Stream, the small-M streaming GEMM (`splits`).
+// tile / splits 0 keep the default choice.
 // Returns false, queueing nothing, when that kernel does not take the call.
-enum { kQ4Pipe = 1, kQ4Skinny = 2, kQ4General = 3, kQ4Big = 4, kQ4Wide = 5 };
+enum { kQ4Pipe = 1, kQ4Skinny = 2, kQ4General = 3, kQ4Big = 4, kQ4Wide = 5, kQ4Stream = 6 };
 bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int splits);
+
+// The small-M streaming Q4 GEMM (q4_gemm_stream): up to 32 rows of fp16 activations on weights
+// with the prefill copy, one block per CU owning a strip of columns over all of K. q4_stream_ok
+// says whether it takes the call; launch_q4_stream splits K only when `split_choice` (or
+// BYHIP_Q4_SPLIT) asks for it.
+bool q4_stream_ok(const GemmArgs& a);
+// Column fragments per block of the streaming GEMM for this call.
+int stream_fn(const GemmArgs& a);
+void launch_q4_stream(const GemmArgs& a, int split_choice = 0);
 
 // Native MXFP4 GEMM (E2M1 x E2M1 with E8M0 block scales): x and w in the FP4-KM packing.
 // K % 128 == 0 is required.

@@ -1815,6 +1815,10 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
         if (!q4_wide_ok(a)) return false;
         launch_q4_skinny(a, splits, true);
         return true;
+    case kQ4Stream:
+        if (fmt != BFormat::Q4Fast || !q4_stream_ok(a)) return false;
+        launch_q4_stream(a, splits);
+        return true;
     case kQ4General:
         if (fmt == BFormat::Q4Fast) launch_f<BFormat::Q4Fast>(a);
         else if (fmt == BFormat::Q4Generic) launch_f<BFormat::Q4Generic>(a);
@@ -1826,6 +1830,17 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
 }
 
 bool q4_f32_wide_takes(const GemmArgs& a) { return q4_wide_f32_ok(a) && env_int("BYHIP_Q4_F32_WIDE", 1) != 0; }
+
+// Whether a call takes the small-M streaming GEMM: fp16 activations, up to 32 rows (or the lower
+// limit BYHIP_Q4_SKINNY_MAX_M sets for the small-M kernels), weights with the prefill copy, at most
+// two column fragments per block and K up to 8192, where it beats the split-K kernels (it loses to
+// the wide tile at 4096 x 28672 and 14336 x 4096, measured at M = 32). BYHIP_Q4_STREAM=0 leaves
+// such calls to the skinny kernel and the wide tile, 1 gives it every shape it takes.
+bool q4_stream_takes(const GemmArgs& a) {
+    const int forced = env_int("BYHIP_Q4_STREAM", -1);
+    if (forced == 0 || a.M > env_int("BYHIP_Q4_SKINNY_MAX_M", 32) || !q4_stream_ok(a)) return false;
+    return forced == 1 || (stream_fn(a) <= 2 && a.K <= 8192);
+}
 
 bool launch_q4_wide_exact_weights(const GemmArgs& a) {
     if (a.M > 32 || !q4_wide_ok(a)) return false;
@@ -1841,6 +1856,10 @@ void launch_gemm(BFormat fmt, const GemmArgs& a) {
     case BFormat::Q4Fast:
         // fp32 activations: the wide tile on two fp16 planes where the scratch holds them
         if (q4_f32_wide_takes(a) && launch_q4_wide_f32(a)) break;
+        if (q4_stream_takes(a)) {
+            launch_q4_stream(a);
+            break;
+        }
         if (q4_skinny_ok(a)) {
             launch_q4_skinny(a, 0, q4_small_wide(a));
             break;

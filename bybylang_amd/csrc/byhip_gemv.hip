@@ -146,12 +146,25 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
         gsel[c] = BLK ? (uint32_t)(c0 + cc) : (uint32_t)(a.group_chunks ? (c0 + cc) / a.group_chunks : 0);
     }
 
-    // 1. the activations this thread stages (chunks tid and tid + 256 of the M x G chunks; with
-    // XHALF half hf = tid & 1 of chunk tid / 2)
-    uint4 xraw[XC][XWL];
+    // 1. the activations this thread stages. fp16: 16-byte pieces tid, tid + 256, ... of the M x G
+    // chunks' 4 M G pieces, so that a wave's loads cover 1 KB of consecutive bytes (whole lines;
+    // loading a chunk's 64 bytes per lane touched four times the lines). fp32: chunks tid and
+    // tid + 256 (with XHALF half hf = tid & 1 of chunk tid / 2).
+    constexpr bool XPIECE = !XF32;
+    constexpr int XP = XPIECE ? M * CPL : 1;  // pieces per thread: 4 M G <= 256 M CPL
+    uint4 xpc[XP];
+    if constexpr (XPIECE) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i) {
+            const int pc = tid + 256 * i, idx = pc >> 2, m = idx / G, ci = idx - m * G;
+            xpc[i] = buf_load16(xr, idx < M * G ? (uint32_t)m * (uint32_t)a.ldx * XB + (uint32_t)(c0 + ci) * 64u + 16u * (pc & 3)
+                                                : kOutOfRange);
+        }
+    }
+    uint4 xraw[XPIECE ? 1 : XC][XWL];
     const int hf = XHALF ? (tid & 1) : 0;
 #pragma unroll
-    for (int i = 0; i < XC; ++i) {
+    for (int i = 0; i < (XPIECE ? 0 : XC); ++i) {
         const int idx = XHALF ? tid >> 1 : tid + 256 * i;
         const int m = idx / G, ci = idx - m * G;
         const uint32_t base = idx < M * G ? (uint32_t)m * (uint32_t)a.ldx * XB + (uint32_t)(c0 + ci) * 32u * XB + 64u * (uint32_t)hf
@@ -255,8 +268,36 @@ __global__ __launch_bounds__(256) void q4_gemv(GemvArgs a) {
             }
         }
     }
+    if constexpr (XPIECE) {
+        // piece t of chunk idx holds x[8 t .. 8 t + 7]: its pairs (x[8t+q], x[8t+q+4]) are piece t
+        // of the staged chunk, and its sums over the low- and high-nibble pairs are added over the
+        // chunk's four lanes (exact products with 1, fp32 accumulation)
+        const h2 one = {1, 1};
 #pragma unroll
-    for (int i = 0; i < (XHALF ? 0 : XC); ++i) {
+        for (int i = 0; i < XP; ++i) {
+            const int pc = tid + 256 * i, idx = pc >> 2, t = pc & 3;
+            const uint32_t A = xpc[i].x, B = xpc[i].y, C = xpc[i].z, D = xpc[i].w;
+            const uint32_t p0 = __builtin_amdgcn_perm(C, A, 0x05040100u), p1 = __builtin_amdgcn_perm(C, A, 0x07060302u);
+            const uint32_t p2 = __builtin_amdgcn_perm(D, B, 0x05040100u), p3 = __builtin_amdgcn_perm(D, B, 0x07060302u);
+            float sl = __builtin_amdgcn_fdot2(bits_h2(p0), one, 0.0f, false);
+            sl = __builtin_amdgcn_fdot2(bits_h2(p2), one, sl, false);
+            float sh = __builtin_amdgcn_fdot2(bits_h2(p1), one, 0.0f, false);
+            sh = __builtin_amdgcn_fdot2(bits_h2(p3), one, sh, false);
+            sl += __shfl_xor(sl, 1, kWave);
+            sh += __shfl_xor(sh, 1, kWave);
+            sl += __shfl_xor(sl, 2, kWave);
+            sh += __shfl_xor(sh, 2, kWave);
+            if (idx < M * G) {
+                reinterpret_cast<uint4*>(xh)[t * M * G + idx] = make_uint4(p0, p1, p2, p3);
+                if (t == 0) {
+                    sums[2 * idx] = 1024.0f * sl + 64.0f * sh;
+                    sums[2 * idx + 1] = sl + sh;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (XHALF || XPIECE ? 0 : XC); ++i) {
         const int idx = tid + 256 * i;
         if (idx < M * G) {
             uint32_t p[16], lo[16];

@@ -16,7 +16,8 @@ enum Q4PlanKind : int {
     kPlanBig = 6,      // the 128 x 256 prefill tile
     kPlanWide = 7,     // the wide tile (128 columns; 16, 32 or 64 rows)
     kPlanExact = 8,    // the exact fp32 MFMA GEMM
-    kPlanLast = kPlanExact
+    kPlanStream = 9,   // the small-M streaming GEMM (M <= 32, one column strip per CU over all of K)
+    kPlanLast = kPlanStream
 };
 struct Q4Plan {
     int kind = 0;

@@ -484,6 +484,7 @@ bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w
     case kPlanSkinny:
     case kPlanGemm:
     case kPlanBig:
+    case kPlanStream:
     case kPlanWide: {
         // fp16 MFMA kernels: only for weights whose products stay in fp16's normal range
         if (!aligned || w->K % 32 != 0 || !w->f16_safe) return false;
@@ -491,6 +492,7 @@ bool q4_run_plan(const Q4Plan& p, const void* x, int x_dtype, const byhip_q4w* w
                          : p.kind == kPlanSkinny ? kQ4Skinny
                          : p.kind == kPlanBig    ? kQ4Big
                          : p.kind == kPlanWide   ? kQ4Wide
+                         : p.kind == kPlanStream ? kQ4Stream
                                                  : kQ4General;
         return launch_q4_choice(q4_fast(w) ? BFormat::Q4Fast : BFormat::Q4Generic,
                                 q4_gemm_args(x, x_dtype, w, y, y_dtype, M), kind, p.tile, p.splits);

@@ -146,10 +146,13 @@ const std::vector<uint8_t>* host_mirror(const void* p) {
     return &it->second.mirror;
 }
 
+std::atomic<unsigned long long> g_alloc_count{0};  // device allocations since the process started
+
 void* device_alloc(size_t bytes) {
     State& s = st();
     void* p = nullptr;
     BYHIP_HIP(hipMalloc(&p, bytes ? bytes : 1));
+    g_alloc_count.fetch_add(1);
     std::lock_guard<std::recursive_mutex> lk(s.mu);
     s.allocs[p].bytes = bytes;
     return p;
@@ -246,6 +249,7 @@ int byhip_init(int device) {
         BYHIP_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
         s.realtime_hz = khz * 1e3;
         BYHIP_HIP(hipMalloc(&s.workspace, kWorkspaceBytes));
+        g_alloc_count.fetch_add(1);
         BYHIP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.gate), sizeof(int), hipHostMallocCoherent));
         *s.gate = 0;
         static_scratch_setup(device);
@@ -775,6 +779,8 @@ extern "C" int byhip_debug_read(const void* src, size_t bytes, void* sink, size_
         BYHIP_LAUNCHED("read_words");
     });
 }
+
+extern "C" unsigned long long byhip_debug_alloc_count(void) { return g_alloc_count.load(); }
 
 extern "C" int byhip_debug_copy(void* dst, const void* src, size_t bytes) {
     return guard([&] {

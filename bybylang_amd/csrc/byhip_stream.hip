@@ -7,15 +7,21 @@
 // leaves most CUs idle. Here one block per CU owns a strip of 16 FN output columns over the whole
 // K, so every weight byte streams from HBM once and the grid fills the chip at any N:
 //   Block: eight waves (two per SIMD). Wave w takes the block's 64-value sub-steps w, w + 8, ...
-//   for all BM rows and all FN column fragments, with private LDS buffers, so the K loop has no
-//   block barrier; the eight partial tiles are added in wave order at the end.
+//   (counted from a per-block starting sub-step, wrapping around) for all BM rows and all FN
+//   column fragments, with private LDS buffers, so the K loop has no block barrier; the eight
+//   partial tiles are added in wave order at the end.
 //   Per sub-step a wave moves the BM activation rows' 128-byte slices straight into one of its
 //   four LDS buffers (1 KB direct loads, whole lines, XOR-swizzled as in the wide tile so the
 //   fragment reads are free of bank conflicts), loads each fragment's 512 contiguous bytes of the
 //   prefill copy (8 bytes per lane) and its fp16 scale, three sub-steps ahead.
 //   The activations are the same for every block and come from L2: per CU that is BM x K x 2 bytes
-//   (256 KB at M = 32, K = 4096), the bound at small N; at large N the weights stream at the HBM
-//   rate.
+//   (256 KB at M = 32, K = 4096), and with at most four sub-steps in flight per wave the K walk is
+//   bound by the L2 latency. Measured at M = 32 (weights rotated past the Infinity Cache, against
+//   the split-K kernels and their sum launch): K x N = 4096 x 4096 6.8-7.0 us against 8.8, 4096 x
+//   6144 8.0-8.3 against 10.4, but 4096 x 28672 (seven fragments per block, dequantization-heavy)
+//   21.3 against 17.1 and 14336 x 4096 15.5-15.9 against 13.1; a per-block starting sub-step and
+//   MFMA / VALU interleaving changed none of these. The router therefore takes it for at most two
+//   fragments per block and K up to 8192.
 #include <algorithm>
 
 #include "byhip_gemm.h"
@@ -28,17 +34,21 @@ namespace {
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 constexpr int kStreamWaves = 8;  // per block, one block per CU
-constexpr int kStreamDepth = 4;  // LDS buffers and register sets per wave: loads three sub-steps ahead
 constexpr int kSub = 64;         // K values per sub-step (the prefill copy's unit)
 constexpr int kMaxFN = 8;        // column fragments per block
 
-template <int FM, int FN>
+// LDS buffers and register sets per wave: loads three sub-steps ahead. (Five buffers at 32 rows
+// and eight at 16, as many as LDS holds, measured the same on the narrow strips: K x N = 4096 x
+// 4096 at M = 32 7.0-7.2 us, 4096 x 6144 8.2-8.6.)
+constexpr int kStreamDepth = 4;
+
+template <int FM, int FN, int D = kStreamDepth>
 struct StreamShape {
     static constexpr int kBM = 16 * FM;
     static constexpr int kXBuf = kBM * kSub * 2;        // one sub-step's activation slices
     static constexpr int kXLoads = kBM / 8;             // 1 KB direct loads per sub-step
     static constexpr int kLoads = kXLoads + 2 * FN;     // with the weights and the scales
-    static constexpr int kLdsX = kStreamWaves * kStreamDepth * kXBuf;
+    static constexpr int kLdsX = kStreamWaves * D * kXBuf;
     static constexpr int kPitch = 16 * FN + 4;          // floats per row of a staged partial tile
     static constexpr int kLdsRed = kStreamWaves * kBM * kPitch * 4;
     static constexpr int kLds = kLdsX > kLdsRed ? kLdsX : kLdsRed;
@@ -54,8 +64,9 @@ struct StreamW {
 
 template <int FM, int FN, int YT>
 __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
-    using S = StreamShape<FM, FN>;
-    constexpr int D = kStreamDepth, BM = S::kBM, L = S::kLoads;
+    constexpr int D = kStreamDepth;
+    using S = StreamShape<FM, FN, D>;
+    constexpr int BM = S::kBM, L = S::kLoads;
     static_assert(S::kLds <= 160 * 1024 && (D - 1) * L <= 63,
                   "q4_gemm_stream: the buffers must fit LDS and the loads in flight the wait counter");
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
@@ -68,9 +79,21 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
     const int nsub = a.part ? min(a.split_steps, (int)nsub_all - s_first) : (int)nsub_all;
     const int nt = nsub > w ? (nsub - w + kStreamWaves - 1) / kStreamWaves : 0;  // this wave's sub-steps
+    // Every block reads the same activations: each starts its K walk at its own sub-step (and wraps
+    // around), so that the blocks sharing an L2 do not all request the same lines at once.
+    const int rot = (int)((blockIdx.x * 5u) % (uint32_t)max(nsub, 1));
+    // sub-step of the wave's t-th (t < nt): (w + 8 t + rot) mod nsub, from the split's first
+    auto sub_of = [&](int t) __attribute__((always_inline)) {
+        int v = w + kStreamWaves * t + rot;
+        v -= v >= nsub ? nsub : 0;
+        v -= v >= nsub ? nsub : 0;
+        return (uint32_t)(s_first + v);
+    };
 
-    // Rows past M, fragments past N and sub-steps past the wave's last read zeros through the range
-    // checks (the launcher keeps every offset below 2^31).
+    // Rows past M and sub-steps past the wave's last read zeros: their per-lane offsets lie past the
+    // resources' sizes (the launcher keeps every offset below 2^31, and the out-of-range marker 2^31
+    // goes into the per-lane offset). Fragments past N are read at the last fragment and never
+    // stored.
     const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.M * K * 2));
     const rsrc_t wr = make_rsrc(a.wpf, (uint32_t)(((size_t)a.N + 15) / 16 * nsub_all * 512));
     const rsrc_t sr = make_rsrc(a.spf, (uint32_t)(((size_t)a.N + 63) / 64 * nsub_all * 256));
@@ -88,23 +111,26 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
     // Fragment reads: lane (c, g) reads row 16 i + c, chunk 2 g + kk, at slot (2 g + kk) ^ x_swizzle(c).
     const int rd0 = 128 * c + 16 * ((2 * g) ^ x_swizzle(c)), rd1 = 128 * c + 16 * ((2 * g + 1) ^ x_swizzle(c));
 
+    const int flast = (a.N + 15) / 16 - 1;
     auto load_x = [&](int t, int buf) __attribute__((always_inline)) {
         const bool ok = t < nt;
-        const uint32_t u = (uint32_t)(s_first + (ok ? w + kStreamWaves * t : 0));
+        const uint32_t u = ok ? sub_of(t) : (uint32_t)s_first;
         const uint32_t oob = ok ? 0u : 0x80000000u;
         uint8_t* const dst = xw + buf * S::kXBuf;
 #pragma unroll
-        for (int q = 0; q < S::kXLoads; ++q) lds_dma16(xr, dst + 1024 * q, xo[q], oob + 128u * u);
+        for (int q = 0; q < S::kXLoads; ++q) lds_dma16(xr, dst + 1024 * q, xo[q] + oob, 128u * u);
     };
     auto load_ws = [&](StreamW<FN>& r, int t) __attribute__((always_inline)) {
         const bool ok = t < nt;
-        const uint32_t u = (uint32_t)(s_first + (ok ? w + kStreamWaves * t : 0));
+        const uint32_t u = ok ? sub_of(t) : (uint32_t)s_first;
         const uint32_t oob = ok ? 0u : 0x80000000u;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const uint32_t f = (uint32_t)(f0 + j);
-            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, 8u * lane, oob + f * wfrag + 512u * u, 0);
-            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff + 2u * (f & 3u), oob + (f >> 2) * squad + 256u * u, 0);
+            const uint32_t f = (uint32_t)min(f0 + j, flast);
+            // default cache policy: marking these loads nontemporal measured slower here (M = 32:
+            // 4096 x 4096 6.8 -> 8.3 us, 14336 x 4096 15.5 -> 20.3)
+            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, 8u * lane + oob, f * wfrag + 512u * u, 0);
+            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff + 2u * (f & 3u) + oob, (f >> 2) * squad + 256u * u, 0);
         }
     };
 
@@ -146,33 +172,56 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
 
     // Sub-steps 0 .. D - 2 are loaded here, sub-step t + D - 1 in sub-step t into the buffer and
     // register set that sub-step t - 1 used (its fragment reads and weights were consumed by its
-    // MFMAs). Loads past the wave's last sub-step read zeros, so every sub-step waits for the same
-    // count: the loads of t + 1 .. t + D - 2 may stay in flight.
+    // MFMAs). Loads past the wave's last sub-step read zeros, so every wait has the same count. A
+    // sub-step runs in two halves: the kk = 0 MFMAs beside the kk = 1 fragment reads, the kk = 1
+    // dequantization and the loads of t + D - 1; the wait for t + 1's loads (those of t + 2 ..
+    // t + D - 1 stay in flight); the kk = 1 MFMAs beside t + 1's kk = 0 reads and dequantization.
+    // Scheduling groups place each MFMA next to its share of the other work.
     StreamW<FN> rs[D];
     static_for<D - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         load_x(k, k);
         load_ws(rs[k], k);
     });
+    h8 x0[FM], x1[FM], b0[FN], b1[FN];
+    wait_vmcnt<(D - 2) * L>();
+    read_x(0, 0, x0);
+    dequant(rs[0], 0, b0);
+    constexpr int kMfmas = FM * FN;  // per half
+    constexpr int kValu = (14 * FN + kMfmas - 1) / kMfmas;
     auto step = [&](int t, auto kc) __attribute__((always_inline)) {
-        constexpr int k = decltype(kc)::value, kp = (k + D - 1) % D;
-        wait_vmcnt<(D - 2) * L>();
+        constexpr int k = decltype(kc)::value, k1 = (k + 1) % D, kp = (k + D - 1) % D;
         __builtin_amdgcn_sched_barrier(0);
-        load_x(t + D - 1, kp);
-        load_ws(rs[kp], t + D - 1);
-        h8 x0[FM], x1[FM], b0[FN], b1[FN];
-        read_x(k, 0, x0);
-        read_x(k, 1, x1);
-        dequant(rs[k], 0, b0);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0[i], b0[j], acc[i][j], 0, 0, 0);
+        read_x(k, 1, x1);
         dequant(rs[k], 1, b1);
+        load_x(t + D - 1, kp);
+        load_ws(rs[kp], t + D - 1);
+#pragma unroll
+        for (int m = 0; m < kMfmas; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
+            if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);       // a fragment read
+            if (m < L) __builtin_amdgcn_sched_group_barrier(0x0010, 1, 0);        // a load
+            __builtin_amdgcn_sched_group_barrier(0x0002, kValu, 0);               // its share of the VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<(D - 2) * L>();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1[i], b1[j], acc[i][j], 0, 0, 0);
+        read_x(k1, 0, x0);
+        dequant(rs[k1], 0, b0);
+#pragma unroll
+        for (int m = 0; m < kMfmas; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);                   // one MFMA
+            if (m < FM) __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);       // a fragment read
+            __builtin_amdgcn_sched_group_barrier(0x0002, kValu, 0);               // its share of the VALU
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
     for (int t0 = 0; t0 < nt; t0 += D) {
@@ -242,6 +291,12 @@ void launch_stream_fm(const GemmArgs& a, int fn, dim3 grid) {
 
 }  // namespace
 
+// Column fragments per block: the fewest that give every CU at most one block.
+int stream_fn(const GemmArgs& a) {
+    const long cus = compute_units(), nfr = (a.N + 15) / 16;
+    return (int)std::min<long>(kMaxFN, std::max<long>(1, (nfr + cus - 1) / cus));
+}
+
 bool q4_stream_ok(const GemmArgs& a) {
     constexpr uint64_t kLim = 0x80000000u;  // offsets stay below 2^31 (the kernel's out-of-range steps)
     return a.x_dtype == BYHIP_F16 && a.wpf && a.spf && a.M >= 1 && a.M <= 32 && a.K % kSub == 0 &&
@@ -249,14 +304,13 @@ bool q4_stream_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 64 * kMaxFN) / 64 * (a.K / kSub) * 256 < kLim;
 }
 
-// Column fragments per block: the fewest that give every CU at most one block (at most 8), so each
-// CU streams one strip of the weights. K is split (fp32 partials, then splitk_sum) only when asked
-// (`split_choice`, or BYHIP_Q4_SPLIT).
+// One strip of stream_fn(a) column fragments per block (at most 8), so each CU streams one strip of
+// the weights. K is split (fp32 partials, then splitk_sum) only when asked (`split_choice`, or
+// BYHIP_Q4_SPLIT).
 void launch_q4_stream(const GemmArgs& a0, int split_choice) {
     GemmArgs a = a0;
-    const long cus = compute_units();
     const long nfr = (a.N + 15) / 16;
-    const int fn = (int)std::min<long>(kMaxFN, std::max<long>(1, (nfr + cus - 1) / cus));
+    const int fn = stream_fn(a);
     const long blocks = (nfr + fn - 1) / fn;
     const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
     const int splits = forced > 1 ? choose_split(a, blocks, a.K / kSub, kStreamWaves, forced, 1) : 1;

@@ -86,6 +86,9 @@ std::string plan_name(const Q4Plan& p) {
         snprintf(buf, sizeof buf, "wide-s%d", p.splits);
         return buf;
     case kPlanExact: return "exact";
+    case kPlanStream:
+        snprintf(buf, sizeof buf, "stream-s%d", p.splits);
+        return buf;
     default: return "none";
     }
 }
@@ -205,6 +208,7 @@ std::vector<Candidate> candidates(int mt, int x_dtype) {
         if (mt <= 32) {
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanSkinny, 0, sp}, 3e-3f});
             for (int sp : {0, 1, 2, 4, 8}) c.push_back({{kPlanWide, 0, sp}, 3e-3f});
+            for (int sp : {0, 2}) c.push_back({{kPlanStream, 0, sp}, 3e-3f});
         }
         if (mt > 32) {
             for (int sp : {0, 1, 2, 4}) c.push_back({{kPlanBig, 0, sp}, 3e-3f});

@@ -303,6 +303,10 @@ int byhip_debug_copy(void* dst, const void* src, size_t bytes);
  * wave stores a fold of what it read into `sink`, which must hold 16 * CUs 32-bit words.
  * No counterpart in the reference. */
 int byhip_debug_read(const void* src, size_t bytes, void* sink, size_t sink_bytes);
+/* The number of device allocations the library has made since the process started (its buffers,
+ * resident weights, workspace and internal temporaries): a test checks with it that an entry
+ * point allocates nothing. No counterpart in the reference. */
+unsigned long long byhip_debug_alloc_count(void);
 
 #ifdef __cplusplus
 }

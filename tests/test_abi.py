@@ -20,7 +20,7 @@ HEADER = os.path.join(ROOT, "include", "byhip.h")
 
 def declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^(?:int|void|double|const char\*|void\*)\s+\**(byhip_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|void|double|unsigned long long|const char\*|void\*)\s+\**(byhip_\w+)\(", text, re.M)))
 
 
 def test_header_and_library_agree():

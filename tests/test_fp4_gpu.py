@@ -12,7 +12,7 @@ import pytest
 
 from oracle_lib import (OP_FP4_COOP_GEMM, f16_tile_program, fp4_coop_lut_word, fp4_tile_program,
                         shape_op_program)
-from parity import (TIER_F32_ACC, bf16_bits_to_f32, f32_to_bf16_rne, max_abs_rel, ref_check,
+from parity import (TIER_BF16_OUT, TIER_F32_ACC, bf16_bits_to_f32, f32_to_bf16_rne, max_abs_rel, ref_check,
                     tier_check)
 
 pytestmark = pytest.mark.gpu
@@ -231,3 +231,34 @@ def test_mxfp4_benchmark_config_rows(hip, oracle):
     wdec = synth.mx_decode(wc, we).astype(np.float64)
     colsum = (xdec.astype(np.float64).sum(axis=0) @ wdec.T)
     tier_check(got.astype(np.float64).sum(axis=0), colsum, 1e-4)
+
+
+def test_mxfp4_benchmark_config_bf16(hip, oracle):
+    """Config 3 exactly as the benchmark runs it: M=2048, K=N=8192, bf16 output. 4 rows against the
+    oracle rounded to bf16 (one bf16 step on top of the fp32-accumulate tier), the same rows equal to
+    the fp32 output rounded to nearest even bit for bit, and the column sums of all rows against an
+    fp64 product of the decoded operands."""
+    M, K, N = 2048, 8192, 8192
+    xb, xdec, wb, table = mx_case(M, K, N, 3)
+    x, w = hip.DeviceBuffer.from_array(xb), hip.DeviceBuffer.from_array(wb)
+    y16 = hip.DeviceBuffer(M * N * 2)
+    print("mxfp4 config 3 bf16", flush=True)
+    hip.mxfp4_gemm(x, w, y16, hip.BF16, M, K, N)
+    bits = y16.read(np.uint16).reshape(M, N)
+    got = bf16_bits_to_f32(bits.reshape(-1)).reshape(M, N)
+    rows = [0, 1, 1027, M - 1]
+    for r in rows:
+        want = oracle.tile_gemm(0, 1, K, N, N * (K // 2), 0, wb, table, xdec[r].copy())
+        tier_check(got[r], f32_to_bf16_rne(want).reshape(-1), TIER_BF16_OUT)
+    y32 = hip.DeviceBuffer(M * N * 4)
+    hip.mxfp4_gemm(x, w, y32, hip.F32, M, K, N)
+    f = y32.read(np.float32).reshape(M, N)
+    for r in rows:
+        assert np.array_equal(bits[r], (f32_to_bf16_rne(f[r]).view(np.uint32) >> 16).astype(np.uint16))
+    from bybylang_amd import synth
+    g = synth.rng(3)
+    _, xc, xe = synth.mxfp4_operand(g, M, K)
+    _, wc, we = synth.mxfp4_operand(g, N, K)
+    wdec = synth.mx_decode(wc, we).astype(np.float64)
+    colsum = xdec.astype(np.float64).sum(axis=0) @ wdec.T
+    tier_check(got.astype(np.float64).sum(axis=0), colsum, TIER_BF16_OUT)

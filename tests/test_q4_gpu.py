@@ -189,6 +189,7 @@ def test_q4_gemm_skinny(hip, oracle, monkeypatch, M, splits, group):
     from bybylang_amd import synth
     K, N = 768, 200
     monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_STREAM", "0")
     if splits:
         monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
     g = synth.rng(7300 + 7 * M + group + splits)
@@ -254,6 +255,58 @@ def test_q4_gemm_wide_small_m(hip, oracle, monkeypatch, M, splits, group):
     assert np.array_equal(got, again)
     want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, group, gpr)
     tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("M", [1, 5, 9, 16, 17, 24, 32])
+@pytest.mark.parametrize("N", [264, 4096 + 40])
+@pytest.mark.parametrize("splits", [0, 3])
+@pytest.mark.parametrize("group", [32, 0])
+def test_q4_gemm_stream(hip, oracle, monkeypatch, M, N, splits, group):
+    """The small-M streaming GEMM (forced: BYHIP_Q4_STREAM=1): ragged M and N (N = 4136 takes two
+    column fragments per block, the last block partly past N), K = 1344 (21 sub-steps of 64, so the
+    eight waves run 2 or 3 each), with and without a K split, fp16 in and out, against the oracle;
+    a repeat call is bit-identical."""
+    from bybylang_amd import synth
+    K = 1344
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_STREAM", "1")
+    if splits:
+        monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
+    g = synth.rng(7900 + 13 * M + group + splits + N)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K, group if group else K)
+    gpr = K // group if group else 1
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 stream M={M} N={N} splits={splits} group={group}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    again, _ = run_q4(hip, x, wq, sc, ze, M, K, N, group, hip.F16, hip.F16, gpr=gpr)
+    assert np.array_equal(got, again)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, group, gpr)
+    tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
+@pytest.mark.parametrize("y_dtype", ["F32", "BF16"])
+@pytest.mark.parametrize("M,K,N", [(32, 4096, 28672), (24, 14336, 4096), (32, 4096, 6144)])
+def test_q4_gemm_stream_layer_shapes(hip, oracle, monkeypatch, y_dtype, M, K, N):
+    """The streaming GEMM (forced) at the layer batch's shapes (7, 1 and 2 column fragments per
+    block; the down projection's K = 14336 as 224 sub-steps, 28 per wave), fp32 and bf16 outputs:
+    4 rows against the oracle, every row against an fp64 product of the fp16-rounded weights."""
+    from bybylang_amd import synth
+    monkeypatch.setenv("BYHIP_Q4_STREAM", "1")
+    g = synth.rng(7950 + M + K // 1024 + N // 1024)
+    wq, sc, ze, codes = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 stream layer M={M} K={K} N={N} y={y_dtype}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, getattr(hip, y_dtype))
+    xf = x.astype(np.float32).reshape(-1)
+    want = oracle.matmul_q4(xf, wq, sc, ze, M, K, N, 32, K // 32, rows=(M - 4, M))[M - 4:M]
+    w = (codes.astype(np.float32) * np.repeat(sc.reshape(N, -1), 32, axis=1)).astype(np.float64)
+    full = x.astype(np.float64) @ w.T
+    if y_dtype == "BF16":
+        tier_check(got[M - 4:M], f32_to_bf16_rne(want).reshape(4, N), TIER_BF16_OUT)
+        tier_check(got, full, TIER_BF16_OUT)
+    else:
+        tier_check(got[M - 4:M], want, TIER_F32_ACC)
+        tier_check(got, full, TIER_F32_ACC)
 
 
 @pytest.mark.parametrize("kind", ["big", "wide"])

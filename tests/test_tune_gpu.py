@@ -58,9 +58,9 @@ def test_prepare_decode_and_prefill(hip, oracle, plans):
         assert hip.q4_prepare(w, M_tune, hip.F16) == 0
         name, cached = hip.q4_plan_info(w, M_tune, hip.F16)
         assert not cached
-        assert name in ("generic", "gemm") or name.split("-")[0] in ("pipe", "skinny", "big", "wide")
+        assert name in ("generic", "gemm") or name.split("-")[0] in ("pipe", "skinny", "big", "wide", "stream")
         if M_tune > 32:
-            assert not name.startswith("skinny-")
+            assert not name.startswith(("skinny-", "stream-"))
         else:
             assert not name.startswith(("big-", "wide-"))
         for M in Ms:

@@ -1,12 +1,13 @@
 """byhip_q4_matmul_static, the Q4 matmul entry point that allocates nothing, against
 byhip_q4_matmul through the C ABI.
 
-The shapes take the routes that use scratch: split-K on the skinny (M = 32) and large-tile
+The shapes take the routes that use scratch: split-K on the small-M (M = 32) and large-tile
 (M = 256) GEMMs, the per-row shifts and fp16 planes of fp32 activations, the exact GEMM's
-split-K, and the GEMV.
+split-K, the GEMV, and the GEMV's K slices (partial sums) at K = 28,672.
 Each shape runs twice in a row on the static entry point, the second time with a smaller input, so
 the second call finds the first call's contents in the shared scratch. Bar: bit-identical to
-byhip_q4_matmul when both take the same split (they share the kernels), else the parity tiers.
+byhip_q4_matmul when both take the same split (they share the kernels), else the parity tiers;
+and the library's count of device allocations is the same before and after every static call.
 """
 import numpy as np
 import pytest
@@ -17,9 +18,13 @@ from parity import REF_TOL, TIER_F32_ACC, ref_check, tier_check
 pytestmark = pytest.mark.gpu
 
 
-def call(hip, fn, x, x_dtype, w, M, N, y_dtype):
+def call(hip, fn, x, x_dtype, w, M, N, y_dtype, no_alloc=False):
     y = hip.DeviceBuffer(M * N * (4 if y_dtype == hip.F32 else 2))
+    lib = _abi.load()
+    before = lib.byhip_debug_alloc_count()
     _abi.check(fn(x.ptr, x_dtype, w.handle, y.ptr, y_dtype, M), "q4 matmul")
+    if no_alloc:
+        assert lib.byhip_debug_alloc_count() == before, "the static entry point allocated device memory"
     return y.read(hip.np_dtype(y_dtype), M * N).astype(np.float32).reshape(M, N)
 
 
@@ -31,6 +36,7 @@ def call(hip, fn, x, x_dtype, w, M, N, y_dtype):
     (48, 12, 1024, 384, "f32", "f32", "tiny"),      # exact GEMM (weights outside fp16), split-K
     (4, 1, 4096, 2048, "f16", "f32", "f16"),        # GEMV (no scratch)
     (6, 3, 4096, 2048, "f32", "f32", "f16"),        # fp32 decode rows on the wide tile
+    (2, 1, 28672, 512, "f32", "f32", "f16"),        # wide tile; then the GEMV in K slices
 ])
 def test_static_entry_matches_q4_matmul(hip, shape):
     M1, M2, K, N, xd, yd, scales = shape
@@ -47,7 +53,7 @@ def test_static_entry_matches_q4_matmul(hip, shape):
         xb = hip.DeviceBuffer.from_array(x.reshape(-1))
         print(f"static entry M={M} K={K} N={N} x={xd} y={yd} scales={scales}", flush=True)
         want = call(hip, lib.byhip_q4_matmul, xb, xt, w, M, N, yt)
-        got = call(hip, lib.byhip_q4_matmul_static, xb, xt, w, M, N, yt)
+        got = call(hip, lib.byhip_q4_matmul_static, xb, xt, w, M, N, yt, no_alloc=True)
         if not np.array_equal(got, want):
             if yd == "f32" and xd == "f32":
                 ref_check(got, want, REF_TOL)
