@@ -114,6 +114,7 @@ __device__ __forceinline__ void store_any(void* y, int y_dtype, size_t idx, floa
 
 template <BFormat F, bool XF32, int BM>
 __global__ __launch_bounds__(256) void gemm_f32_exact(GemmArgs a) {
+    if (a.gate && *a.gate != a.gate_want) return;  // the other route was chosen (whole grid)
     constexpr int FM = BM / 16;      // row fragments per wave
     constexpr int FX = BM / 4;       // activations a thread stages per step
     constexpr int XT = EBK / FX;     // threads per activation row

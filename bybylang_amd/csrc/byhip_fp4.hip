@@ -78,6 +78,20 @@ bool table_products_are_halves(const float* t) {
     return ok;
 }
 
+// Device-side form of table_products_are_halves: thread b checks the 16 products with scale entry
+// b (finite, and exact in fp16), and the block's AND goes to *flag (1: the products are halves).
+__global__ __launch_bounds__(256) void fp4km_classify(const float* __restrict__ t, int* flag) {
+    const float s = t[16 + threadIdx.x];
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float p = t[i] * s;
+        ok = ok && __builtin_isfinite(p) && (float)(_Float16)p == p;
+    }
+    ok = __syncthreads_and(ok);
+    if (threadIdx.x == 0) *flag = ok ? 1 : 0;
+}
+
 void fp4km_run(const void* x, int x_dtype, const uint8_t* blob, size_t blob_bytes, size_t scale_base,
                const float* lut, size_t lut_floats, size_t lut_base, void* y, int y_dtype, int M,
                int K, int N) {
@@ -108,14 +122,31 @@ void fp4km_run(const void* x, int x_dtype, const uint8_t* blob, size_t blob_byte
     GemmArgs a;
     a.x = x; a.x_dtype = x_dtype; a.y = y; a.y_dtype = y_dtype; a.M = M; a.K = K; a.N = N;
     a.blob = blob; a.scale_base = scale_base; a.lut = lut + lut_base;
-    // The fp16 MFMA kernel when every decoded weight is a half (the table is read from its host
-    // copy, or from the device outside a recording); otherwise the exact fp32 GEMM.
-    float t[272];
+    // The fp16 MFMA kernel when every decoded weight is a half, otherwise the exact fp32 GEMM. The
+    // table is classified on the host from its host copy, outside recordings; otherwise on the
+    // device, by a kernel that writes the choice to a flag, with both routes queued behind it and
+    // each gated on the flag, so that a recording replays the right route for whatever table the
+    // buffer holds at replay, and no call waits for the device to read the table.
     const bool aligned = reinterpret_cast<uintptr_t>(blob) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
-    if (aligned && env_int("BYHIP_TILE_EXACT", 0) == 0 && try_read_small(lut, lut_base * 4, t, sizeof t) &&
-        table_products_are_halves(t)) {
-        launch_gemm(BFormat::Fp4Km, a);
-        return;
+    if (aligned && env_int("BYHIP_TILE_EXACT", 0) == 0) {
+        float t[272];
+        if (!session_recording() && mirror_read(lut, lut_base * 4, t, sizeof t)) {
+            if (table_products_are_halves(t)) {
+                launch_gemm(BFormat::Fp4Km, a);
+                return;
+            }
+        } else {
+            int* flag = device_flags();
+            launch("fp4km_classify", fp4km_classify, dim3(1), dim3(256), 0, static_cast<const float*>(lut + lut_base),
+                   flag);
+            GemmArgs g = a;
+            g.gate = flag;
+            g.gate_want = 1;
+            launch_gemm(BFormat::Fp4Km, g);
+            g.gate_want = 0;
+            launch_gemm_exact(BFormat::Fp4Km, g);
+            return;
+        }
     }
     if (reinterpret_cast<uintptr_t>(blob) % 16 != 0)
         unsupported("byhip: tile GEMM needs 16-byte aligned weights");
@@ -236,6 +267,7 @@ int byhip_fp4km_tile_gemm(const void* x, int x_dtype, const uint8_t* blob, size_
                           void* y, int y_dtype, int M, int K, int N) {
     return guard([&] {
         enter_compute();
+        note_device_write(y);
         fp4km_run(x, x_dtype, blob, blob_bytes, scale_base, lut, lut_floats, lut_base, y, y_dtype, M, K, N);
     });
 }
@@ -252,6 +284,7 @@ int byhip_mxfp4_gemm(const uint8_t* x, const uint8_t* w, void* y, int y_dtype, i
         check_span(y, (size_t)M * N * dtype_bytes(y_dtype), "MXFP4 output");
         if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
             fail("byhip: MXFP4 operands must be 16-byte aligned");
+        note_device_write(y);
         launch_mxfp4(x, x + xb, w, w + wb, y, y_dtype, M, K, N);
     });
 }
@@ -260,6 +293,7 @@ int byhip_f16_tile_gemm(const void* x, int x_dtype, const uint16_t* w, size_t w_
                         int y_dtype, int M, int K, int N) {
     return guard([&] {
         enter_compute();
+        note_device_write(y);
         f16_run(x, x_dtype, w, w_halves, y, y_dtype, M, K, N);
     });
 }
@@ -285,6 +319,7 @@ int byhip_program_dispatch(const uint32_t* words, int n_words, void* mem, size_t
         enter_compute();
         // The reference's checks in its order (cpu_vm.c:178-188, 420-628), with its messages.
         if (!words || n_words <= 0 || !mem || mem_len == 0) fail("invalid CPU VM arguments");
+        note_device_write(mem);
         const uint32_t w0 = words[0], op = w0 & 0xFFu, fmt = reg_a(w0);
         if (op != 0xB0 && op != 0xAC && op != 0xAA && op != 0xAB)
             unsupported("byhip: program op 0x%02x is not a tile GEMM / Q4 / FP4 shape op", op);

@@ -58,6 +58,11 @@ struct GemmArgs {
     // The wide tile on fp32 activations: x holds the high fp16 plane of the shifted activations and
     // x_lo the low one (x * 2^t = hi + lo, t per row in row_shift).
     const void* x_lo = nullptr;
+    // A device-side route choice: when gate is set, the general fp16 MFMA GEMM, the exact GEMM and
+    // their split-K sum do nothing unless *gate == gate_want (the flag a classification kernel
+    // earlier on the stream wrote), so two routes can be queued and only the chosen one runs.
+    const int* gate = nullptr;
+    int gate_want = 0;
 };
 
 // Whether 8-output chunks may leave as 16-byte stores: every row of y (or of the split-K

@@ -215,6 +215,7 @@ __device__ __forceinline__ void stage_b(const GemmArgs& a, int n, int k0g, const
 
 template <BFormat F, bool XF32, int YT>
 __global__ __launch_bounds__(256) void gemm_f16_mfma(GemmArgs a) {
+    if (a.gate && *a.gate != a.gate_want) return;  // the other route was chosen (whole grid)
     constexpr int PERM = FormatTraits<F>::kPerm;
     // fp32 activations with Q4 weights: the weights' fp16 remainders too (F16 weights and FP4-KM
     // tables of halves are exact in one fp16 term)
@@ -559,12 +560,13 @@ __global__ __launch_bounds__(256) void q4_gemm_pipe(GemmArgs a) {
 }
 
 // y = sum over z of part[z] (z in order, so the result does not depend on block timing), four
-// consecutive outputs per thread.
+// consecutive outputs per thread; nothing when `gate` is set and *gate != want (GemmArgs::gate).
 // The same sum, one output per thread: four times the blocks, for outputs too few to fill the CUs
 // four to a thread.
 template <int YT>
 __global__ __launch_bounds__(256) void splitk_sum1(const float* __restrict__ part, int splits, int M, int N,
-                                                   void* y) {
+                                                   void* y, const int* gate, int want) {
+    if (gate && *gate != want) return;
     const size_t mn = (size_t)M * N, stride = splitk_stride(M, N);
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= mn) return;
@@ -583,7 +585,8 @@ __global__ __launch_bounds__(256) void splitk_sum1(const float* __restrict__ par
 
 template <int YT>
 __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part, int splits, int M, int N,
-                                                  void* y) {
+                                                  void* y, const int* gate, int want) {
+    if (gate && *gate != want) return;
     const size_t mn = (size_t)M * N, stride = splitk_stride(M, N);
     const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
@@ -1505,17 +1508,17 @@ void launch_splitk_sum(const GemmArgs& a, int splits) {
     if (grid.x < (unsigned)compute_units()) {  // fp32 route M = 9 .. 32: 0.2-0.4 us faster
         const dim3 g1((unsigned)(((size_t)a.M * a.N + 255) / 256));
         switch (a.y_dtype) {
-        case BYHIP_F32: launch("splitk_sum1", splitk_sum1<BYHIP_F32>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
-        case BYHIP_F16: launch("splitk_sum1", splitk_sum1<BYHIP_F16>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
-        default: launch("splitk_sum1", splitk_sum1<BYHIP_BF16>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
+        case BYHIP_F32: launch("splitk_sum1", splitk_sum1<BYHIP_F32>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y, a.gate, a.gate_want); break;
+        case BYHIP_F16: launch("splitk_sum1", splitk_sum1<BYHIP_F16>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y, a.gate, a.gate_want); break;
+        default: launch("splitk_sum1", splitk_sum1<BYHIP_BF16>, g1, dim3(256), 0, a.part, splits, a.M, a.N, a.y, a.gate, a.gate_want); break;
         }
         BYHIP_LAUNCHED("splitk_sum1");
         return;
     }
     switch (a.y_dtype) {
-    case BYHIP_F32: launch("splitk_sum", splitk_sum<BYHIP_F32>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
-    case BYHIP_F16: launch("splitk_sum", splitk_sum<BYHIP_F16>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
-    default: launch("splitk_sum", splitk_sum<BYHIP_BF16>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y); break;
+    case BYHIP_F32: launch("splitk_sum", splitk_sum<BYHIP_F32>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y, a.gate, a.gate_want); break;
+    case BYHIP_F16: launch("splitk_sum", splitk_sum<BYHIP_F16>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y, a.gate, a.gate_want); break;
+    default: launch("splitk_sum", splitk_sum<BYHIP_BF16>, grid, dim3(256), 0, a.part, splits, a.M, a.N, a.y, a.gate, a.gate_want); break;
     }
     BYHIP_LAUNCHED("splitk_sum");
 }

@@ -101,6 +101,15 @@ void read_small(const void* p, size_t off, void* dst, size_t bytes);
 // The same, but returns false instead of waiting when there is no host copy and a session is being
 // recorded (a recording cannot wait for the device).
 bool try_read_small(const void* p, size_t off, void* dst, size_t bytes);
+// Reads from the host copy only (false when there is none): no device access, no wait.
+bool mirror_read(const void* p, size_t off, void* dst, size_t bytes);
+// A kernel of the library writes the buffer holding p: its host copy no longer holds its contents.
+void note_device_write(const void* p);
+// Whether a session is being recorded (graph capture or kept launches).
+bool session_recording();
+// A small device array of the library (64 ints), for flags that one kernel writes and later
+// kernels on the stream read (the FP4-KM route's table classification).
+int* device_flags();
 
 template <class F>
 int guard(F&& f) {

@@ -569,6 +569,7 @@ int byhip_q4_resident_info(const byhip_q4w* w, byhip_q4w_info* out) {
 int byhip_q4_matmul(const void* x, int x_dtype, const byhip_q4w* w, void* y, int y_dtype, int M) {
     return guard([&] {
         enter_compute();
+        note_device_write(y);
         q4_matmul_impl(x, x_dtype, w, y, y_dtype, M, false, nullptr, 0);
     });
 }
@@ -601,6 +602,7 @@ int byhip_q4_matmul_fused(int mode, const float* a, byhip_q4w* const* ws, int n_
         for (int i = 0; i < n_out; ++i) check_span(outs[i], (size_t)ws[i]->N * 4, "fused GEMV output");
         if (has_res) check_span(res, (size_t)(mode == 1 ? ws[0]->N : max_n) * 4, "fused GEMV residual");
         if (has_norm) check_span(gamma, (size_t)K * 4, "fused GEMV norm weights");
+        for (int i = 0; i < n_out; ++i) note_device_write(outs[i]);
         launch_q4_gemv_fused(mode, a, ws, n_ws, outs, has_res ? res : nullptr, has_norm ? gamma : nullptr, eps);
     });
 }

@@ -52,6 +52,7 @@ struct State {
     std::vector<Recording> recordings;  // id -> recording
     int last_recording = -1;
     int* gate = nullptr;   // pinned host word the replay gate waits on (hipHostMalloc, coherent)
+    int* flags = nullptr;  // device_flags(): 64 ints, allocated by byhip_init
     int gate_open = 0;     // value that opens the next gate
 };
 
@@ -186,6 +187,33 @@ void check_span(const void* p, size_t need, const char* what) {
     // Not one of ours (memory from another allocator): the caller vouches for the size.
 }
 
+bool mirror_read(const void* p, size_t off, void* dst, size_t bytes) {
+    State& s = st();
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
+    auto it = s.allocs.find(p);
+    if (it == s.allocs.end() || off + bytes > it->second.mirror.size()) return false;
+    memcpy(dst, it->second.mirror.data() + off, bytes);
+    return true;
+}
+
+void note_device_write(const void* p) {
+    if (!p) return;
+    State& s = st();
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
+    for (auto& kv : s.allocs) {
+        const uint8_t* base = static_cast<const uint8_t*>(kv.first);
+        const uint8_t* q = static_cast<const uint8_t*>(p);
+        if (q >= base && q < base + (kv.second.bytes ? kv.second.bytes : 1)) {
+            kv.second.mirror.clear();
+            return;
+        }
+    }
+}
+
+bool session_recording() { return st().recording; }
+
+int* device_flags() { return st().flags; }
+
 bool try_read_small(const void* p, size_t off, void* dst, size_t bytes) {
     if (const std::vector<uint8_t>* m = host_mirror(p)) {
         if (off + bytes <= m->size()) {
@@ -249,7 +277,8 @@ int byhip_init(int device) {
         BYHIP_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
         s.realtime_hz = khz * 1e3;
         BYHIP_HIP(hipMalloc(&s.workspace, kWorkspaceBytes));
-        g_alloc_count.fetch_add(1);
+        BYHIP_HIP(hipMalloc(reinterpret_cast<void**>(&s.flags), 64 * sizeof(int)));
+        g_alloc_count.fetch_add(2);
         BYHIP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.gate), sizeof(int), hipHostMallocCoherent));
         *s.gate = 0;
         static_scratch_setup(device);

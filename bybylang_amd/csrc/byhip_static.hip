@@ -49,6 +49,7 @@ extern "C" int byhip_q4_matmul_static(const void* x, int x_dtype, const byhip_q4
         if (x_dtype == BYHIP_F32 && M > 8 && (size_t)M * sizeof(int) > kStaticScratchBytes)
             fail("byhip: byhip_q4_matmul_static takes at most %zu rows of fp32 activations (M=%d)",
                  kStaticScratchBytes / sizeof(int), M);
+        note_device_write(y);
         q4_matmul_run_scratch(x, x_dtype, w, y, y_dtype, M, p, kStaticScratchBytes);
     });
 }
