@@ -11,6 +11,10 @@
         span from the end of its first mark to the start of its second, and per kernel the dispatch
         count and average / min / max duration
 
+    python -m bybylang_amd.profile_summary regions DB --timed
+        the same for every second region only, in one table with short kernel names: bench.py's
+        recordings run once when they are made and once timed, so these are the timed replays
+
     python -m bybylang_amd.profile_summary traffic --fetch DB --write DB --copy-bytes N
                                                    --kernel SUBSTRING [--json OUT]
         HBM bytes per dispatch of the kernel whose name contains SUBSTRING, from a FETCH_SIZE run
@@ -73,6 +77,33 @@ def kernel_regions(db: str):
         stats = [(k, len(v), sum(v) / len(v), min(v), max(v)) for k, v in per.items()]
         out.append((b0 - a1, sorted(stats, key=lambda r: -r[1] * r[2])))
     return out
+
+
+def short_name(name: str) -> str:
+    """A kernel's name without namespaces, return type and parameter list: `q4_gemv<1, 2, ...>`.
+    A mangled name (`_ZN5byhip12_GLOBAL__N_114split_rows_f16E...`) gives its last nested part."""
+    if name.startswith("_ZN"):
+        parts, i = [], 3
+        while i < len(name) and name[i].isdigit():
+            j = i
+            while name[j].isdigit():
+                j += 1
+            n = int(name[i:j])
+            parts.append(name[j:j + n])
+            i = j + n
+        return parts[-1] if parts else name
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for k, ch in enumerate(name):  # cut at the parameter list: the first "(" outside <...>
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and k > 0 and name[k - 1] != ":" and name[k - 1] != " ":
+            name = name[:k]
+            break
+    return name.replace("byhip::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
 
 
 def counter_per_dispatch(db: str, counter: str):
@@ -143,6 +174,7 @@ def main(argv=None) -> int:
     t.add_argument("--between-marks", action="store_true")
     g = sub.add_parser("regions")
     g.add_argument("db")
+    g.add_argument("--timed", action="store_true")
     r = sub.add_parser("traffic")
     r.add_argument("--fetch", required=True)
     r.add_argument("--write", required=True)
@@ -158,6 +190,16 @@ def main(argv=None) -> int:
             print(f"`{name[:110]}`: {vals['dispatches']} dispatches, {vals['avg_us']:.2f} us")
             for k in sorted(v for v in vals if v not in ("dispatches", "avg_us")):
                 print(f"  {k} = {vals[k]:.4g}")
+        return 0
+    if a.cmd == "regions" and a.timed:
+        print("| region | span us | kernel | dispatches | avg us | min us | max us |\n"
+              "|---:|---:|---|---:|---:|---:|---:|")
+        for i, (span, stats) in enumerate(kernel_regions(a.db)):
+            if i % 2 == 0:
+                continue
+            for j, (name, n, avg, mn, mx) in enumerate(stats):
+                head = f"| {i} | {span / 1e3:.2f}" if j == 0 else "| |"
+                print(f"{head} | `{short_name(name)}` | {n} | {avg / 1e3:.3f} | {mn / 1e3:.3f} | {mx / 1e3:.3f} |")
         return 0
     if a.cmd == "regions":
         for i, (span, stats) in enumerate(kernel_regions(a.db)):
