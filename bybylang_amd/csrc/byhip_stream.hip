@@ -127,10 +127,17 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const uint32_t f = (uint32_t)min(f0 + j, flast);
-            // default cache policy: marking these loads nontemporal measured slower here (M = 32:
-            // 4096 x 4096 6.8 -> 8.3 us, 14336 x 4096 15.5 -> 20.3)
-            r.w[j] = __builtin_amdgcn_raw_buffer_load_b64(wr, 8u * lane + oob, f * wfrag + 512u * u, 0);
-            r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff + 2u * (f & 3u) + oob, (f >> 2) * squad + 256u * u, 0);
+            // Default cache policy: marking these loads nontemporal measured slower here (M = 32:
+            // 4096 x 4096 6.8 -> 8.3 us, 14336 x 4096 15.5 -> 20.3). Issued as assembly, so the
+            // compiler's wait-count pass does not see them: through the K loop's back edge it
+            // placed waits of vmcnt 2 to 11 before their first use, which drained the loads of
+            // the sub-steps ahead in every sub-step. The K loop's explicit waits cover them (loads
+            // complete in issue order: a register set is read only after the wait that follows
+            // its sub-step's loads), and the sets stay live past the final wait.
+            asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen"
+                         : "=v"(r.w[j]) : "v"(8u * lane + oob), "s"(wr), "s"(f * wfrag + 512u * u));
+            asm volatile("buffer_load_ushort %0, %1, %2, %3 offen"
+                         : "=v"(r.s[j]) : "v"(soff + 2u * (f & 3u) + oob), "s"(sr), "s"((f >> 2) * squad + 256u * u));
         }
     };
 
@@ -224,17 +231,25 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
     };
+    // Whole groups of D sub-steps, so the loop body has no branch around a step (a step past the
+    // wave's last reads zeros, whose products add nothing): the register sets then keep one place
+    // through the back edge and every step issues the same loads.
     for (int t0 = 0; t0 < nt; t0 += D) {
         static_for<D>([&](auto kc) {
             const int t = t0 + decltype(kc)::value;
-            if (t < nt) step(t, kc);
+            step(t, kc);
         });
     }
 
     // Partial tiles -> LDS in output layout once every load has landed (those past the last
-    // sub-step wrote zeros into the buffers) and every wave is done with its buffers -> the eight
-    // partials added in wave order -> y or the split-K partials.
+    // sub-step wrote zeros into the buffers and registers) and every wave is done with its buffers
+    // -> the eight partials added in wave order -> y or the split-K partials. The register sets
+    // are kept live until the loads into them have landed.
     wait_vmcnt<0>();
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) asm volatile("" ::"v"(rs[k].w[j]), "v"(rs[k].s[j]));
     __syncthreads();
     constexpr int P = S::kPitch;
     float* red = reinterpret_cast<float*>(lds);  // [waves][BM rows][P]
