@@ -172,8 +172,10 @@ bool launch_q4_choice(BFormat fmt, const GemmArgs& a, int kind, int tile, int sp
 // says whether it takes the call; launch_q4_stream splits K only when `split_choice` (or
 // BYHIP_Q4_SPLIT) asks for it.
 bool q4_stream_ok(const GemmArgs& a);
-// Column fragments per block of the streaming GEMM for this call.
-int stream_fn(const GemmArgs& a);
+// Column fragments per block of the streaming GEMM for this call with `row_blocks` blocks per
+// strip, and the row blocks it launches (2 for 17 to 32 rows unless BYHIP_Q4_STREAM_HALVES=0).
+int stream_fn(const GemmArgs& a, int row_blocks);
+int stream_row_blocks(const GemmArgs& a);
 void launch_q4_stream(const GemmArgs& a, int split_choice = 0);
 
 // Native MXFP4 GEMM (E2M1 x E2M1 with E8M0 block scales): x and w in the FP4-KM packing.

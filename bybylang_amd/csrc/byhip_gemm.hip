@@ -1836,13 +1836,13 @@ bool q4_f32_wide_takes(const GemmArgs& a) { return q4_wide_f32_ok(a) && env_int(
 
 // Whether a call takes the small-M streaming GEMM: fp16 activations, up to 32 rows (or the lower
 // limit BYHIP_Q4_SKINNY_MAX_M sets for the small-M kernels), weights with the prefill copy, at most
-// two column fragments per block and K up to 8192, where it beats the split-K kernels (it loses to
-// the wide tile at 4096 x 28672 and 14336 x 4096, measured at M = 32). BYHIP_Q4_STREAM=0 leaves
+// two column fragments per 32-row block and K up to 8192, where it beats the split-K kernels (it
+// loses to the wide tile at 4096 x 28672 and 14336 x 4096, measured at M = 32). BYHIP_Q4_STREAM=0 leaves
 // such calls to the skinny kernel and the wide tile, 1 gives it every shape it takes.
 bool q4_stream_takes(const GemmArgs& a) {
     const int forced = env_int("BYHIP_Q4_STREAM", -1);
     if (forced == 0 || a.M > env_int("BYHIP_Q4_SKINNY_MAX_M", 32) || !q4_stream_ok(a)) return false;
-    return forced == 1 || (stream_fn(a) <= 2 && a.K <= 8192);
+    return forced == 1 || (stream_fn(a, 1) <= 2 && a.K <= 8192);
 }
 
 bool launch_q4_wide_exact_weights(const GemmArgs& a) {

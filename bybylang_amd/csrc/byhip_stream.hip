@@ -62,9 +62,8 @@ struct StreamW {
     uint32_t s[FN];
 };
 
-template <int FM, int FN, int YT>
+template <int FM, int FN, int YT, int D = kStreamDepth>
 __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
-    constexpr int D = kStreamDepth;
     using S = StreamShape<FM, FN, D>;
     constexpr int BM = S::kBM, L = S::kLoads;
     static_assert(S::kLds <= 160 * 1024 && (D - 1) * L <= 63,
@@ -74,6 +73,8 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, g = lane >> 4;
     const int f0 = blockIdx.x * FN;  // the block's first column fragment
+    const int m0 = (int)blockIdx.y * BM;  // the block's first activation row
+    if (16 * f0 >= a.N) return;  // a block of the grid's rounding (whole block, before any barrier)
     const int K = a.K;
     const uint32_t nsub_all = (uint32_t)K / kSub;
     const int s_first = a.part ? (int)blockIdx.z * a.split_steps : 0;
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < S::kXLoads; ++q) {
         const int r = 8 * q + (lane >> 3), chunk = (lane & 7) ^ x_swizzle(r);
-        xo[q] = (uint32_t)r * (uint32_t)K * 2u + 16u * chunk;
+        xo[q] = (uint32_t)(m0 + r) * (uint32_t)K * 2u + 16u * chunk;
     }
     const uint32_t wfrag = nsub_all * 512u, squad = nsub_all * 256u;
     // the lane's scale in a quad's [2][16][4] block: its 32-value group g / 2, column c
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
     constexpr int kChunks = BM * 2 * FN;  // 8 outputs each
     for (int u = threadIdx.x; u < kChunks; u += 512) {
         const int row = u / (2 * FN), col = (u % (2 * FN)) * 8;
-        if (row >= a.M) continue;
+        if (m0 + row >= a.M) continue;
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = 0.0f;
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
             v[0] += s0.x; v[1] += s0.y; v[2] += s0.z; v[3] += s0.w;
             v[4] += s1.x; v[5] += s1.y; v[6] += s1.z; v[7] += s1.w;
         }
-        store_out8<YT>(a, part, vec, row, 16 * f0 + col, v);
+        store_out8<YT>(a, part, vec, m0 + row, 16 * f0 + col, v);
     }
 }
 
@@ -306,10 +307,18 @@ void launch_stream_fm(const GemmArgs& a, int fn, dim3 grid) {
 
 }  // namespace
 
-// Column fragments per block: the fewest that give every CU at most one block.
-int stream_fn(const GemmArgs& a) {
+// Row blocks: 17 to 32 rows run as two blocks of 16 rows over the same strip (each reads half the
+// activations; the two share an XCD, so the second read of the strip's weights comes from its L2),
+// unless BYHIP_Q4_STREAM_HALVES=0 keeps one block of 32 rows.
+int stream_row_blocks(const GemmArgs& a) {
+    return a.M > 16 && env_int("BYHIP_Q4_STREAM_HALVES", 1) != 0 ? 2 : 1;
+}
+
+// Column fragments per block with `row_blocks` blocks per strip: the fewest that give every CU at
+// most one block.
+int stream_fn(const GemmArgs& a, int row_blocks) {
     const long cus = compute_units(), nfr = (a.N + 15) / 16;
-    return (int)std::min<long>(kMaxFN, std::max<long>(1, (nfr + cus - 1) / cus));
+    return (int)std::min<long>(kMaxFN, std::max<long>(1, (nfr * row_blocks + cus - 1) / cus));
 }
 
 bool q4_stream_ok(const GemmArgs& a) {
@@ -319,19 +328,24 @@ bool q4_stream_ok(const GemmArgs& a) {
            (uint64_t)(a.N + 64 * kMaxFN) / 64 * (a.K / kSub) * 256 < kLim;
 }
 
-// One strip of stream_fn(a) column fragments per block (at most 8), so each CU streams one strip of
-// the weights. K is split (fp32 partials, then splitk_sum) only when asked (`split_choice`, or
-// BYHIP_Q4_SPLIT).
+// One strip of stream_fn column fragments (at most 8) per block and row block, so each CU streams
+// one strip of the weights. Block (x, y) takes strip x and rows 16 y .. 16 y + 15 (or all 32 rows in
+// one block). Blocks go to the XCDs round-robin in dispatch order (x first), so with two row blocks
+// the strip count is rounded up to a multiple of 8 (the extra blocks exit at once) and the two
+// blocks of a strip land on one XCD. K is split (fp32 partials, then splitk_sum) only when asked
+// (`split_choice`, or BYHIP_Q4_SPLIT).
 void launch_q4_stream(const GemmArgs& a0, int split_choice) {
     GemmArgs a = a0;
     const long nfr = (a.N + 15) / 16;
-    const int fn = stream_fn(a);
-    const long blocks = (nfr + fn - 1) / fn;
+    const int rb = stream_row_blocks(a);
+    const int fn = stream_fn(a, rb);
+    const long strips = (nfr + fn - 1) / fn;
+    const long blocks = rb == 2 ? (strips + 7) / 8 * 8 : strips;
     const int forced = split_choice > 0 ? split_choice : env_int("BYHIP_Q4_SPLIT", 0);
-    const int splits = forced > 1 ? choose_split(a, blocks, a.K / kSub, kStreamWaves, forced, 1) : 1;
+    const int splits = forced > 1 ? choose_split(a, strips * rb, a.K / kSub, kStreamWaves, forced, 1) : 1;
     if (splits == 1) a.part = nullptr;
-    const dim3 grid((unsigned)blocks, 1, (unsigned)splits);
-    if (a.M <= 16) launch_stream_fm<1>(a, fn, grid);
+    const dim3 grid((unsigned)blocks, (unsigned)rb, (unsigned)splits);
+    if (a.M <= 16 || rb == 2) launch_stream_fm<1>(a, fn, grid);
     else launch_stream_fm<2>(a, fn, grid);
     BYHIP_LAUNCHED("q4_gemm_stream");
     if (a.part) launch_splitk_sum(a, splits);

@@ -284,6 +284,28 @@ def test_q4_gemm_stream(hip, oracle, monkeypatch, M, N, splits, group):
     tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
 
 
+@pytest.mark.parametrize("M", [17, 32])
+@pytest.mark.parametrize("N", [264, 4096 + 40])
+@pytest.mark.parametrize("splits", [0, 3])
+def test_q4_gemm_stream_one_row_block(hip, oracle, monkeypatch, M, N, splits):
+    """Above 16 rows the streaming GEMM runs each strip as two 16-row blocks; BYHIP_Q4_STREAM_HALVES=0
+    keeps one 32-row block per strip. That geometry against the oracle, as above."""
+    from bybylang_amd import synth
+    K = 1344
+    monkeypatch.setenv("BYHIP_Q4_ROUTE", "2")
+    monkeypatch.setenv("BYHIP_Q4_STREAM", "1")
+    monkeypatch.setenv("BYHIP_Q4_STREAM_HALVES", "0")
+    if splits:
+        monkeypatch.setenv("BYHIP_Q4_SPLIT", str(splits))
+    g = synth.rng(7930 + M + splits + N)
+    wq, sc, ze, _ = synth.q4_weights(g, N, K)
+    x = synth.activations(g, M, K, np.float16)
+    print(f"q4 stream one row block M={M} N={N} splits={splits}", flush=True)
+    got, _ = run_q4(hip, x, wq, sc, ze, M, K, N, 32, hip.F16, hip.F16)
+    want = oracle.matmul_q4(x.astype(np.float32).reshape(-1), wq, sc, ze, M, K, N, 32, K // 32)
+    tier_check(got, want.astype(np.float16).astype(np.float32), TIER_F32_ACC)
+
+
 @pytest.mark.parametrize("y_dtype", ["F32", "BF16"])
 @pytest.mark.parametrize("M,K,N", [(32, 4096, 28672), (24, 14336, 4096), (32, 4096, 6144)])
 def test_q4_gemm_stream_layer_shapes(hip, oracle, monkeypatch, y_dtype, M, K, N):
