@@ -192,7 +192,15 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
         load_ws(rs[k], k);
     });
     h8 x0[FM], x1[FM], b0[FN], b1[FN];
+    // The weight loads are not tracked by the compiler, so their results look ready at once: after
+    // the wait that covers a register set, the set passes through an empty asm statement, which no
+    // use of it can be placed before.
+    auto landed = [&](StreamW<FN>& r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) asm volatile("" : "+v"(r.w[j]), "+v"(r.s[j]));
+    };
     wait_vmcnt<(D - 2) * L>();
+    landed(rs[0]);
     read_x(0, 0, x0);
     dequant(rs[0], 0, b0);
     constexpr int kMfmas = FM * FN;  // per half
@@ -217,6 +225,7 @@ __global__ __launch_bounds__(512, 1) void q4_gemm_stream(GemmArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<(D - 2) * L>();
+        landed(rs[k1]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
