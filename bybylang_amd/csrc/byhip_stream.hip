@@ -5,7 +5,8 @@
 // At small M the weights dominate the bytes, and a GEMM tile that covers only part of K (split-K)
 // pays a second launch for the partial sums, while a tile that covers all of K but few columns
 // leaves most CUs idle. Here one block per CU owns a strip of 16 FN output columns over the whole
-// K, so every weight byte streams from HBM once and the grid fills the chip at any N:
+// K, so every weight byte streams from HBM once and the grid fills the chip at any N. From 17 rows
+// a strip has two 16-row blocks on one XCD (the second read of its weights hits that XCD's L2):
 //   Block: eight waves (two per SIMD). Wave w takes the block's 64-value sub-steps w, w + 8, ...
 //   (counted from a per-block starting sub-step, wrapping around) for all BM rows and all FN
 //   column fragments, with private LDS buffers, so the K loop has no block barrier; the eight
@@ -15,13 +16,14 @@
 //   fragment reads are free of bank conflicts), loads each fragment's 512 contiguous bytes of the
 //   prefill copy (8 bytes per lane) and its fp16 scale, three sub-steps ahead.
 //   The activations are the same for every block and come from L2: per CU that is BM x K x 2 bytes
-//   (256 KB at M = 32, K = 4096), and with at most four sub-steps in flight per wave the K walk is
-//   bound by the L2 latency. Measured at M = 32 (weights rotated past the Infinity Cache, against
-//   the split-K kernels and their sum launch): K x N = 4096 x 4096 6.8-7.0 us against 8.8, 4096 x
-//   6144 8.0-8.3 against 10.4, but 4096 x 28672 (seven fragments per block, dequantization-heavy)
-//   21.3 against 17.1 and 14336 x 4096 15.5-15.9 against 13.1; a per-block starting sub-step and
-//   MFMA / VALU interleaving changed none of these. The router therefore takes it for at most two
-//   fragments per block and K up to 8192.
+//   (128 KB per 16-row block at K = 4096). The weight and scale loads are inline assembly, outside
+//   the compiler's wait-count tracking, which had drained the loads ahead in every sub-step; the K
+//   loop's explicit waits cover them. Measured at M = 32 (weights rotated past the Infinity Cache,
+//   against the split-K kernels and their sum launch): K x N = 4096 x 4096 6.6 us against 8.8,
+//   4096 x 6144 8.0 against 10.4, but 4096 x 28672 (seven fragments per block, dequantization-
+//   heavy) 21.3 against 17.1 and 14336 x 4096 15.5-15.9 against 13.1 (the last two before the load
+//   change). The router therefore takes it for at most two fragments per 32-row block and K up to
+//   8192.
 #include <algorithm>
 
 #include "byhip_gemm.h"
