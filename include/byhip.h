@@ -233,8 +233,8 @@ int byhip_q4_plans_reset(void);
  * Returns BYHIP_UNSUPPORTED, with the outputs untouched, for the combinations the reference's
  * encoders reject (n_ws outside 1..3, n_outs < n_ws, mode 1 without exactly two weights, a missing
  * output, residual or norm buffer) and for weights this kernel does not take (mismatched shapes
- * or scale formats, K % 32 != 0, K > 8192): the caller then runs the unfused sequence, as the
- * reference's callers do. */
+ * or scale formats, K % 32 != 0); any K that is a multiple of 32 is taken (long rows in K slices).
+ * The caller then runs the unfused sequence, as the reference's callers do. */
 int byhip_q4_matmul_fused(int mode, const float* a, byhip_q4w* const* ws, int n_ws, float* const* outs,
                           int n_outs, const float* res, int has_res, const float* gamma, float eps,
                           int has_norm);
